@@ -1,0 +1,228 @@
+/*
+ * vortx_hip.h — C ABI of the MI355X (gfx950) linalg hot path.
+ *
+ * Drop-in boundary for vortx's GEMM op on tensor views
+ * (reference: src/linalg/gemm.rs:34-321, src/shapes.rs:51-60) plus a
+ * GGUF block-quantized dequant-GEMV (Q8_0, Q4_0, Q4_K) that the reference
+ * does not have. Plain pointers and sizes only; no C++ or HIP types cross
+ * this boundary. Device pointers are HIP device addresses; streams are
+ * hipStream_t values passed as void*.
+ *
+ * Conventions shared by every entry point:
+ *  - Every function returns a vx_status (0 == VX_OK). Nothing throws.
+ *    vx_last_error_message() gives a human-readable reason for the last
+ *    failure on the calling thread; vx_last_hip_error() the hipError_t.
+ *  - Launches are asynchronous on the given stream (NULL = null stream).
+ *    The caller keeps every buffer alive until the stream work completes;
+ *    the library never frees or retains caller memory.
+ *  - A vx_ctx is immutable after vx_init and may be shared by threads.
+ */
+#ifndef VORTX_HIP_H
+#define VORTX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Status codes                                                        */
+/* ------------------------------------------------------------------ */
+typedef enum vx_status {
+    VX_OK = 0,
+    /* Operand shapes are incompatible. The reference panics on the same
+     * condition (assert_eq!, src/linalg/gemm.rs:70-104); a Rust shim maps
+     * this code to panic!. */
+    VX_ERR_SHAPE = 1,
+    /* Valid request that this build does not support (rank > 4, an index
+     * beyond 2^63, K not a multiple of the block size, ...). */
+    VX_ERR_UNSUPPORTED = 2,
+    /* Invalid argument: NULL pointer, unknown quant type, bad axis. */
+    VX_ERR_INVALID = 3,
+    /* A HIP runtime call failed; vx_last_hip_error() returns its code.
+     * Maps to the reference's Err(GpuBackendError). */
+    VX_ERR_HIP = 4,
+    /* The embedded gfx950 code object failed to load (hipModuleLoadData). */
+    VX_ERR_NO_CODE_OBJECT = 5
+} vx_status;
+
+/* ------------------------------------------------------------------ */
+/* Tensor views                                                        */
+/* ------------------------------------------------------------------ */
+
+/* Byte-compatible with vortx's TensorLayout (src/shapes.rs:51-60):
+ * sizes and strides in ELEMENTS, row-major, rank <= 4, offset in elements
+ * from the buffer base. Dimensions at index >= rank are ignored. */
+typedef struct vx_layout {
+    uint32_t size[4];
+    uint32_t stride[4];
+    uint32_t rank;
+    uint32_t offset;
+} vx_layout;
+
+/* Read-only f32 view = TensorRef<f32> (src/tensor/tensor_ref.rs:11-14).
+ * `base` is the buffer start; the element at index (i0,i1,i2,i3) lives at
+ * base[offset + sum_k i_k * stride[k]] (offset applied like
+ * TensorRef::buffer(), src/tensor/tensor_ref.rs:101-103). */
+typedef struct vx_cview {
+    const float* base;
+    vx_layout layout;
+} vx_cview;
+
+/* Writable f32 view = TensorMut<f32> (src/tensor/tensor_mut.rs:10-13). */
+typedef struct vx_mview {
+    float* base;
+    vx_layout layout;
+} vx_mview;
+
+/* GGML type ids of the supported block formats. */
+typedef enum vx_qtype {
+    VX_Q4_0 = 2,  /* 32 weights / 18 bytes: f16 d, 16 B of nibbles      */
+    VX_Q8_0 = 8,  /* 32 weights / 34 bytes: f16 d, 32 int8              */
+    VX_Q4_K = 12  /* 256 weights / 144 bytes: f16 d, f16 dmin, 12 B of
+                     6-bit scales/mins, 128 B of nibbles               */
+} vx_qtype;
+
+/* A row-major block-quantized matrix W[rows, cols]: each row is cols/QK
+ * consecutive blocks, rows are row_stride_bytes apart. This is a GGUF
+ * tensor with ne = [cols, rows] (vortx maps ggml dim 0 to its column
+ * dimension: GGML_IDS, src/shapes.rs:15-18). */
+typedef struct vx_qweight {
+    const void* base;
+    uint32_t qtype;             /* a vx_qtype */
+    uint32_t rows;              /* M */
+    uint32_t cols;              /* K, a multiple of the block size */
+    uint32_t reserved;          /* must be 0 */
+    uint64_t row_stride_bytes;  /* >= (cols/QK) * block_bytes */
+} vx_qweight;
+
+typedef struct vx_context* vx_ctx;
+typedef void* vx_stream; /* hipStream_t */
+
+/* ------------------------------------------------------------------ */
+/* Context                                                             */
+/* ------------------------------------------------------------------ */
+
+/* Loads the embedded gfx950 code objects on `device` (hipModuleLoadData)
+ * and resolves every kernel. Counterpart of Gemm::from_backend (khal
+ * #[derive(Shader)], used at src/linalg/gemm.rs:366). */
+int vx_init(int device, vx_ctx* out_ctx);
+int vx_destroy(vx_ctx ctx);
+/* Device ordinal and compute-unit count the context was built for. */
+int vx_device_info(vx_ctx ctx, int* device, int* num_cus);
+
+/* ------------------------------------------------------------------ */
+/* GEMM: out = lhs * rhs, f32                                          */
+/* ------------------------------------------------------------------ */
+
+/* Replaces Gemm::dispatch (src/linalg/gemm.rs:47-187). Each view is
+ * canonicalized to rank 4 [n, c, rows, cols] (TensorLayout::canonicalize,
+ * src/shapes.rs:145-155); n and c must match across the three operands,
+ * out is [.., M, N], lhs [.., M, K], rhs [.., K, N]. Arbitrary strides
+ * (transposed views included). Kernel choice by shape: the naive kernel
+ * when M < 32 and N < 32 (the reference's rule, :111-112), an f32 GEMV
+ * when N == 1, otherwise the MFMA tiled kernel. out is only written. */
+int vx_gemm_f32(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                const vx_cview* lhs, const vx_cview* rhs);
+
+/* Replaces Gemm::dispatch_naive (src/linalg/gemm.rs:190-246): forces the
+ * one-thread-per-output kernel with sequential-k f32 accumulation (the
+ * order of gemm_naive, vortx-shaders/src/linalg/gemm.rs:196-237). Unlike
+ * the reference this variant validates shapes. */
+int vx_gemm_f32_naive(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                      const vx_cview* lhs, const vx_cview* rhs);
+
+/* Replaces Gemm::dispatch_tiled (src/linalg/gemm.rs:249-305): forces the
+ * MFMA tiled kernel (never the GEMV route). Validates shapes. */
+int vx_gemm_f32_tiled(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                      const vx_cview* lhs, const vx_cview* rhs);
+
+/* Kernel route vx_gemm_f32 takes for these views, without launching
+ * (host logic only; usable without a GPU). */
+typedef enum vx_gemm_route {
+    VX_ROUTE_NAIVE = 0,
+    VX_ROUTE_TILED = 1,
+    VX_ROUTE_GEMV = 2,
+    VX_ROUTE_EMPTY = 3 /* M, N or a batch size is 0: nothing to launch */
+} vx_gemm_route;
+int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
+                      const vx_cview* rhs, int* route);
+
+/* ------------------------------------------------------------------ */
+/* Block-quantized GEMV: y = W * x   (no reference counterpart)        */
+/* ------------------------------------------------------------------ */
+
+/* y[m, b] = sum_k W[m, k] * x[k, b] with W decoded exactly from its
+ * blocks and f32 accumulation. y is an [M, B] view, x a [K, B] view
+ * (rank 1 views mean B = 1); any strides. Fast path: x with stride 1
+ * along K (activations stored [B, K]). Same operand roles as
+ * Gemm::dispatch(out = y, lhs = W, rhs = x). */
+int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
+              const vx_qweight* w, const vx_cview* x);
+
+/* vx_gemv_q with options; flags is a bitwise OR of vx_gemv_flags.
+ * By default every launch multiplies the exactly decoded weights with f32 x
+ * (f32 FMA accumulation). VX_GEMV_X_INT8 (batch-1 launches) instead splits
+ * each 32-element block of x into two int8 levels with one f32 scale,
+ * x ~= c (254 x1 + x2) with |error| <= c/2 ~ 1.6e-5 max|x_block|, reduces
+ * each weight block exactly in int32 (v_dot4_i32_i8) and combines blocks in
+ * f32. */
+typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1 } vx_gemv_flags;
+int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
+                 const vx_qweight* w, const vx_cview* x, uint32_t flags);
+
+/* out[m, k] = W[m, k] decoded to f32 (bit-exact: every block value is
+ * exactly representable in f32). out is an [M, K] view, any strides. */
+int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                  const vx_qweight* w);
+
+/* Block geometry of a vx_qtype: weights per block and bytes per block. */
+int vx_qtype_info(uint32_t qtype, uint32_t* block_weights,
+                  uint32_t* block_bytes);
+
+/* ------------------------------------------------------------------ */
+/* Layout algebra (host only) — TensorLayout, src/shapes.rs            */
+/* ------------------------------------------------------------------ */
+
+/* TensorLayout::contiguous (src/shapes.rs:85-99). rank <= 4. */
+int vx_layout_contiguous(const uint32_t* size, uint32_t rank, vx_layout* out);
+/* TensorLayout::canonicalize (src/shapes.rs:145-155): prepend size-1
+ * dims to rank 4; the offset is reset to 0 exactly as the reference does
+ * (the view offset is carried by the buffer slice instead). */
+int vx_layout_canonicalize(const vx_layout* in, vx_layout* out);
+/* TensorLayout::transpose (src/shapes.rs:238-254). */
+int vx_layout_transpose(const vx_layout* in, uint32_t axis_a,
+                        uint32_t axis_b, vx_layout* out);
+/* TensorLayout::broadcast (src/shapes.rs:346-391): VX_ERR_SHAPE when the
+ * shapes are incompatible (the reference returns None). */
+int vx_layout_broadcast(const vx_layout* a, const vx_layout* b,
+                        vx_layout* a_out, vx_layout* b_out);
+/* TensorLayout::view (src/shapes.rs:407-441). `strides` may be NULL; a
+ * stride of 0xFFFFFFFF means None (use the contiguous default). */
+int vx_layout_view(const vx_layout* in, uint32_t offset,
+                   const uint32_t* shape, uint32_t rank,
+                   const uint32_t* strides, uint32_t nstrides, vx_layout* out);
+/* TensorLayout::narrow (src/shapes.rs:443-464). */
+int vx_layout_narrow(const vx_layout* in, uint32_t axis, uint32_t first,
+                     uint32_t count, vx_layout* out);
+/* TensorLayout::unsqueeze (src/shapes.rs:161-178). */
+int vx_layout_unsqueeze(const vx_layout* in, uint32_t axis, vx_layout* out);
+/* TensorLayout::is_contiguous (src/shapes.rs:332-343): 1 or 0. */
+int vx_layout_is_contiguous(const vx_layout* in);
+
+/* ------------------------------------------------------------------ */
+/* Errors                                                              */
+/* ------------------------------------------------------------------ */
+const char* vx_status_string(int status);
+/* Message of the last failure on this thread ("" if none). */
+const char* vx_last_error_message(void);
+/* hipError_t of the last VX_ERR_HIP on this thread (0 if none). */
+int vx_last_hip_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VORTX_HIP_H */

@@ -1,0 +1,346 @@
+/*
+ * vx_oracle.c — CPU ORACLE for the vortx linalg hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker, never the product:
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load it. The product path (libvortx_hip.so) neither links nor calls it.
+ *
+ * What it restates, and what pins each part (checks live in tests/):
+ *
+ *  - orc_f16_to_f32: IEEE-754 binary16 -> binary32, from the format's
+ *    definition. Pinned exhaustively (all 65536 bit patterns) against
+ *    numpy's float16 conversion.
+ *  - orc_dequant_*: GGML block formats Q8_0 / Q4_0 / Q4_K (public ggml
+ *    block_q8_0 / block_q4_0 / block_q4_K layout). The reference has NO
+ *    quantized code (no file to cite), so relative to the reference this is
+ *    "parity unpinned"; the decode is pinned instead by hand-built known-
+ *    answer blocks with literal expected values (tests/golden), one-hot
+ *    position sweeps, exact scale linearity and cross-format identities.
+ *  - orc_gemm_ref_f32: the f32 summation order of the reference kernels,
+ *    gemm_naive (vortx-shaders/src/linalg/gemm.rs:225-235: sum += l*r over
+ *    k, sequential) and gemm_tiled (:84-171: per output acc += a*b over
+ *    k, tile after tile; zero padding adds +0 which leaves the value
+ *    unchanged). Built with -ffp-contract=off: one rounding per mul and per
+ *    add. Index math follows Shape::it (vortx-shaders/src/linalg/shape.rs:
+ *    46-48) in 64 bits. Pinned against numpy float64 matmul (BLAS) and the
+ *    closed forms identity / zero / K=0 / K=1 / integer-exact products.
+ *  - orc_gemm_f64: the same contraction accumulated in double (the parity
+ *    reference for GPU outputs, tolerance stated in each test).
+ *  - orc_gemv_q_f64: y = W x over exactly decoded weights, in double.
+ *  - orc_gemm_tiled_f32_omp / orc_gemv_q_f32_omp: CPU-parallel restatements
+ *    used only as bench.py's cpu_baseline ("port"): the first keeps
+ *    gemm_tiled's 64x64x16 tiling and k order with one output tile per
+ *    OpenMP task (vortx-shaders/src/linalg/gemm.rs:14-34, 84-192); the second
+ *    is a dequant-dot with no reference equivalent.
+ *
+ * oracle/_ref: the reference is Rust (crate vortx 0.3.0 + rust-gpu shaders,
+ * Cargo.toml:1-58) and this image has no Rust toolchain and no crates.io
+ * registry, so the reference itself is unbuildable here; nothing is built
+ * into oracle/_ref.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_Q4_0 2
+#define ORC_Q8_0 8
+#define ORC_Q4_K 12
+
+/* ---------------------------------------------------------------- */
+/* binary16 -> binary32                                             */
+/* ---------------------------------------------------------------- */
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) & 1u;
+    const uint32_t e = (uint32_t)(h >> 10) & 0x1Fu;
+    const uint32_t m = (uint32_t)h & 0x3FFu;
+    float mag;
+    if (e == 0) {
+        /* zero or subnormal: m * 2^-24, exact in f32 */
+        mag = ldexpf((float)m, -24);
+    } else if (e == 31) {
+        mag = m ? NAN : INFINITY;
+    } else {
+        /* normal: (1024 + m) * 2^(e - 25), exact in f32 */
+        mag = ldexpf((float)(1024u + m), (int)e - 25);
+    }
+    return sign ? -mag : mag;
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+int orc_qtype_info(uint32_t qtype, uint32_t* qk, uint32_t* bytes) {
+    switch (qtype) {
+    case ORC_Q4_0: *qk = 32; *bytes = 18; return 0;
+    case ORC_Q8_0: *qk = 32; *bytes = 34; return 0;
+    case ORC_Q4_K: *qk = 256; *bytes = 144; return 0;
+    default: return -1;
+    }
+}
+
+/* ---------------------------------------------------------------- */
+/* Block decoders (one block -> QK floats)                          */
+/* ---------------------------------------------------------------- */
+
+/* block_q8_0 { half d; int8 qs[32]; }  value_i = d * qs[i] */
+static void dq_q8_0(const uint8_t* blk, float* out) {
+    const float d = orc_f16_to_f32(rd16(blk));
+    for (int i = 0; i < 32; ++i) out[i] = d * (float)(int8_t)blk[2 + i];
+}
+
+/* block_q4_0 { half d; uint8 qs[16]; }
+ * value_j = (lo(qs[j]) - 8) * d, value_{j+16} = (hi(qs[j]) - 8) * d */
+static void dq_q4_0(const uint8_t* blk, float* out) {
+    const float d = orc_f16_to_f32(rd16(blk));
+    for (int j = 0; j < 16; ++j) {
+        const uint8_t q = blk[2 + j];
+        out[j] = (float)((int)(q & 0xF) - 8) * d;
+        out[j + 16] = (float)((int)(q >> 4) - 8) * d;
+    }
+}
+
+/* 6-bit scale and min of sub-block s (0..7) from the 12 packed bytes. */
+void orc_q4k_scale_min(const uint8_t* sc12, int s, uint8_t* sc, uint8_t* mn) {
+    if (s < 4) {
+        *sc = sc12[s] & 63;
+        *mn = sc12[s + 4] & 63;
+    } else {
+        *sc = (uint8_t)((sc12[s + 4] & 0xF) | ((sc12[s - 4] >> 6) << 4));
+        *mn = (uint8_t)((sc12[s + 4] >> 4) | ((sc12[s] >> 6) << 4));
+    }
+}
+
+/* block_q4_K { half d; half dmin; uint8 scales[12]; uint8 qs[128]; }
+ * chunk c (0..3) = qs[32c .. 32c+32): low nibbles -> sub-block 2c
+ * (elements 64c + l), high nibbles -> sub-block 2c+1 (elements 64c+32+l).
+ * value = (d*sc)*q - (dmin*m). Both products are exact in f32; the
+ * subtraction rounds once. */
+static void dq_q4_k(const uint8_t* blk, float* out) {
+    const float d = orc_f16_to_f32(rd16(blk));
+    const float dmin = orc_f16_to_f32(rd16(blk + 2));
+    const uint8_t* sc12 = blk + 4;
+    const uint8_t* qs = blk + 16;
+    for (int c = 0; c < 4; ++c) {
+        uint8_t sc0, m0, sc1, m1;
+        orc_q4k_scale_min(sc12, 2 * c, &sc0, &m0);
+        orc_q4k_scale_min(sc12, 2 * c + 1, &sc1, &m1);
+        const float d0 = d * (float)sc0, mm0 = dmin * (float)m0;
+        const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        for (int l = 0; l < 32; ++l) {
+            const uint8_t q = qs[32 * c + l];
+            out[64 * c + l] = d0 * (float)(q & 0xF) - mm0;
+            out[64 * c + 32 + l] = d1 * (float)(q >> 4) - mm1;
+        }
+    }
+}
+
+static int dq_block(uint32_t qtype, const uint8_t* blk, float* out) {
+    switch (qtype) {
+    case ORC_Q4_0: dq_q4_0(blk, out); return 0;
+    case ORC_Q8_0: dq_q8_0(blk, out); return 0;
+    case ORC_Q4_K: dq_q4_k(blk, out); return 0;
+    default: return -1;
+    }
+}
+
+/* W[M, K] (rows row_stride bytes apart) -> out[M*K] row-major f32. */
+int orc_dequant(uint32_t qtype, const uint8_t* w, uint32_t M, uint32_t K,
+                uint64_t row_stride, float* out) {
+    uint32_t qk, bb;
+    if (orc_qtype_info(qtype, &qk, &bb)) return -1;
+    if (K % qk) return -2;
+    const uint32_t nb = K / qk;
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; ++m) {
+        const uint8_t* row = w + (uint64_t)m * row_stride;
+        for (uint32_t b = 0; b < nb; ++b)
+            dq_block(qtype, row + (uint64_t)b * bb, out + (uint64_t)m * K + (uint64_t)b * qk);
+    }
+    return 0;
+}
+
+/* y[m*ys_m + b*ys_b] = sum_k W[m,k] * x[k*xs_k + b*xs_b], in double. */
+int orc_gemv_q_f64(uint32_t qtype, const uint8_t* w, uint32_t M, uint32_t K,
+                   uint64_t row_stride, const float* x, int64_t xs_k,
+                   int64_t xs_b, uint32_t B, double* y, int64_t ys_m,
+                   int64_t ys_b) {
+    uint32_t qk, bb;
+    if (orc_qtype_info(qtype, &qk, &bb)) return -1;
+    if (K % qk) return -2;
+    const uint32_t nb = K / qk;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t m = 0; m < (int64_t)M; ++m) {
+        float blk[256];
+        double acc[64];
+        for (uint32_t b0 = 0; b0 < B; b0 += 64) {
+            const uint32_t bn = (B - b0) < 64 ? (B - b0) : 64;
+            for (uint32_t b = 0; b < bn; ++b) acc[b] = 0.0;
+            const uint8_t* row = w + (uint64_t)m * row_stride;
+            for (uint32_t ib = 0; ib < nb; ++ib) {
+                dq_block(qtype, row + (uint64_t)ib * bb, blk);
+                for (uint32_t i = 0; i < qk; ++i) {
+                    const int64_t k = (int64_t)ib * qk + i;
+                    for (uint32_t b = 0; b < bn; ++b)
+                        acc[b] += (double)blk[i] * (double)x[k * xs_k + (int64_t)(b0 + b) * xs_b];
+                }
+            }
+            for (uint32_t b = 0; b < bn; ++b) y[m * ys_m + (int64_t)(b0 + b) * ys_b] = acc[b];
+        }
+    }
+    return 0;
+}
+
+/* CPU baseline: f32 dequant-dot, OpenMP over rows, x contiguous [B, K]. */
+int orc_gemv_q_f32_omp(uint32_t qtype, const uint8_t* w, uint32_t M, uint32_t K,
+                       uint64_t row_stride, const float* x, uint32_t B, float* y,
+                       int nthreads) {
+    uint32_t qk, bb;
+    if (orc_qtype_info(qtype, &qk, &bb)) return -1;
+    if (K % qk || B > 64) return -2;
+    const uint32_t nb = K / qk;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#endif
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < (int64_t)M; ++m) {
+        float blk[256];
+        float acc[64];
+        for (uint32_t b = 0; b < B; ++b) acc[b] = 0.0f;
+        const uint8_t* row = w + (uint64_t)m * row_stride;
+        for (uint32_t ib = 0; ib < nb; ++ib) {
+            dq_block(qtype, row + (uint64_t)ib * bb, blk);
+            for (uint32_t b = 0; b < B; ++b) {
+                const float* xb = x + (uint64_t)b * K + (uint64_t)ib * qk;
+                float s = 0.0f;
+                for (uint32_t i = 0; i < qk; ++i) s += blk[i] * xb[i];
+                acc[b] += s;
+            }
+        }
+        for (uint32_t b = 0; b < B; ++b) y[(uint64_t)m * B + b] = acc[b];
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------- */
+/* GEMM on canonical rank-4 views                                    */
+/* ---------------------------------------------------------------- */
+
+/* A canonical [n, c, h, w] view: element (i0,i1,i2,i3) at
+ * base[i0*s0 + i1*s1 + i2*s2 + i3*s3] (Shape::it, shape.rs:46-48). */
+typedef struct orc_view {
+    const float* base;
+    uint32_t size[4];
+    int64_t stride[4];
+} orc_view;
+
+static inline float at(const orc_view* v, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return v->base[(int64_t)a * v->stride[0] + (int64_t)b * v->stride[1] +
+                   (int64_t)c * v->stride[2] + (int64_t)d * v->stride[3]];
+}
+
+/* out (f32 view, written through `out_base` with its strides) =
+ * lhs * rhs in the reference's f32 order: per output, sum starts at +0
+ * and adds l*r for k = 0..K-1 sequentially, one rounding per op. */
+int orc_gemm_ref_f32(float* out_base, const int64_t* out_stride,
+                     const orc_view* lhs, const orc_view* rhs) {
+    const uint32_t N0 = lhs->size[0], C = lhs->size[1], M = lhs->size[2], K = lhs->size[3];
+    const uint32_t N = rhs->size[3];
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int64_t bn = 0; bn < (int64_t)N0; ++bn)
+        for (int64_t bc = 0; bc < (int64_t)C; ++bc)
+            for (uint32_t i = 0; i < M; ++i)
+                for (uint32_t j = 0; j < N; ++j) {
+                    float sum = 0.0f;
+                    for (uint32_t k = 0; k < K; ++k) {
+                        const float p = at(lhs, bn, bc, i, k) * at(rhs, bn, bc, k, j);
+                        sum = sum + p;
+                    }
+                    out_base[bn * out_stride[0] + bc * out_stride[1] + (int64_t)i * out_stride[2] +
+                             (int64_t)j * out_stride[3]] = sum;
+                }
+    return 0;
+}
+
+/* Double-precision contraction. out is a dense [n, c, nrows_sel, N]
+ * array. rows == NULL selects every row; otherwise only rows[r],
+ * r < nrows (used to check large GPU outputs on a sample of rows). */
+int orc_gemm_f64(double* out, const orc_view* lhs, const orc_view* rhs,
+                 const uint32_t* rows, uint32_t nrows) {
+    const uint32_t N0 = lhs->size[0], C = lhs->size[1], M = lhs->size[2], K = lhs->size[3];
+    const uint32_t N = rhs->size[3];
+    const uint32_t R = rows ? nrows : M;
+#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+    for (int64_t bn = 0; bn < (int64_t)N0; ++bn)
+        for (int64_t bc = 0; bc < (int64_t)C; ++bc)
+            for (int64_t r = 0; r < (int64_t)R; ++r) {
+                const uint32_t i = rows ? rows[r] : (uint32_t)r;
+                double* o = out + ((bn * C + bc) * (int64_t)R + r) * N;
+                for (uint32_t j = 0; j < N; ++j) o[j] = 0.0;
+                for (uint32_t k = 0; k < K; ++k) {
+                    const double a = (double)at(lhs, bn, bc, i, k);
+                    for (uint32_t j = 0; j < N; ++j) o[j] += a * (double)at(rhs, bn, bc, k, j);
+                }
+            }
+    (void)M;
+    return 0;
+}
+
+/* CPU baseline: restatement of gemm_tiled (vortx-shaders/src/linalg/
+ * gemm.rs:41-194) for contiguous row-major A [M,K], B [K,N], C [M,N].
+ * One OpenMP task per 64x64 output tile; inside a task the 256
+ * "invocations" of a workgroup run one after another between the two
+ * barriers, with the same 64x16 / 16x64 staging (padded strides 17 and 65)
+ * and the same k order. */
+int orc_gemm_tiled_f32_omp(float* c, const float* a, const float* b, uint32_t M,
+                           uint32_t N, uint32_t K, int nthreads) {
+    enum { TM = 64, TN = 64, TK = 16, SA = TK + 1, SB = TN + 1 };
+    const uint32_t tiles_m = (M + TM - 1) / TM, tiles_n = (N + TN - 1) / TN;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#endif
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t t = 0; t < (int64_t)tiles_m * tiles_n; ++t) {
+        const uint32_t tile_row = (uint32_t)(t / tiles_n) * TM;
+        const uint32_t tile_col = (uint32_t)(t % tiles_n) * TN;
+        float sa[TM * SA], sb[TK * SB];
+        float acc[TM][TN];
+        memset(acc, 0, sizeof(acc));
+        for (uint32_t kt = 0; kt < K; kt += TK) {
+            for (uint32_t r = 0; r < TM; ++r)
+                for (uint32_t q = 0; q < TK; ++q) {
+                    const uint32_t gr = tile_row + r, gc = kt + q;
+                    sa[r * SA + q] = (gr < M && gc < K) ? a[(uint64_t)gr * K + gc] : 0.0f;
+                }
+            for (uint32_t r = 0; r < TK; ++r)
+                for (uint32_t q = 0; q < TN; ++q) {
+                    const uint32_t gr = kt + r, gc = tile_col + q;
+                    sb[r * SB + q] = (gr < K && gc < N) ? b[(uint64_t)gr * N + gc] : 0.0f;
+                }
+            for (uint32_t i = 0; i < TM; ++i)
+                for (uint32_t kk = 0; kk < TK; ++kk) {
+                    const float av = sa[i * SA + kk];
+                    for (uint32_t j = 0; j < TN; ++j) acc[i][j] = acc[i][j] + av * sb[kk * SB + j];
+                }
+        }
+        for (uint32_t i = 0; i < TM; ++i) {
+            const uint32_t row = tile_row + i;
+            if (row >= M) continue;
+            for (uint32_t j = 0; j < TN; ++j) {
+                const uint32_t col = tile_col + j;
+                if (col < N) c[(uint64_t)row * N + col] = acc[i][j];
+            }
+        }
+    }
+    return 0;
+}
+
+int orc_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

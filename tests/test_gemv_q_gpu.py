@@ -1,0 +1,195 @@
+"""Block-quantized GEMV and dequantize on the GPU vs the CPU oracle.
+
+Decode must be bit-exact (every Q8_0 / Q4_0 / Q4_K weight is exactly
+representable in f32); GEMV outputs must be within normwise 1e-3 of the
+float64 oracle. The reference has no quantized path, so these are pinned by
+the oracle, itself pinned in tests/test_oracle.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+import vortx_amd as vx
+from oracle import oracle as O
+from tests.helpers import assert_close, note
+from vortx_amd import synthetic as S
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+QTYPES = [vx.VX_Q4_0, vx.VX_Q8_0, vx.VX_Q4_K]
+QN = {vx.VX_Q4_0: "q4_0", vx.VX_Q8_0: "q8_0", vx.VX_Q4_K: "q4_k"}
+
+
+def _special_scales(w: np.ndarray, qtype: int) -> np.ndarray:
+    """Overwrite some block scales with edge values: f16 subnormals, -0,
+    negative, zero, the largest finite half."""
+    qk, bb = O.QTYPE_INFO[qtype]
+    M, rb = w.shape
+    blocks = w.reshape(M, rb // bb, bb).copy()
+    specials = np.array([0x0001, 0x03FF, 0x8000, 0xBC00, 0x0000, 0x7BFF, 0x0400, 0x8001], dtype=np.uint16)
+    for i, s in enumerate(specials):
+        r, b = i % M, (3 * i) % blocks.shape[1]
+        blocks[r, b, 0] = s & 0xFF
+        blocks[r, b, 1] = s >> 8
+        if qtype == vx.VX_Q4_K:  # dmin too
+            blocks[r, b, 2] = specials[-1 - i] & 0xFF
+            blocks[r, b, 3] = specials[-1 - i] >> 8
+    return blocks.reshape(M, rb)
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_dequantize_bit_exact(qgemv, qtype):
+    M, K = 37, 1024
+    note(f"dequantize {QN[qtype]} {M}x{K}")
+    w = _special_scales(S.quant_weights(qtype, M, K, seed=11).numpy(), qtype)
+    wd = torch.from_numpy(w).to(DEV)
+    out = torch.full((M, K), float("nan"), device=DEV)
+    qgemv.dequantize(out, vx.QWeight(wd, qtype, M, K))
+    torch.cuda.synchronize()
+    ref = O.dequant(qtype, w, M, K)
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), "decode differs from the oracle bit pattern"
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_dequantize_strided_output(qgemv, qtype):
+    M, K = 9, 512
+    note(f"dequantize strided {QN[qtype]}")
+    w = S.quant_weights(qtype, M, K, seed=12)
+    big = torch.full((K, 2 * M), float("nan"), device=DEV)
+    out_view = big[:, 1::2].t()  # [M, K] with strides (2, 2M)
+    qgemv.dequantize(out_view, vx.QWeight(w.to(DEV), qtype, M, K))
+    torch.cuda.synchronize()
+    ref = O.dequant(qtype, w.numpy(), M, K)
+    assert np.array_equal(out_view.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert torch.isnan(big[:, 0::2]).all(), "wrote outside the view"
+
+
+def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False):
+    w = S.quant_weights(qtype, M, K, seed=seed, device=DEV)
+    x = S.activations(B, K, seed=seed + 1, device=DEV)
+    y = torch.full((B, M), float("nan"), device=DEV) if y_out is None else y_out
+    xv = x.t() if x_kb is None else x_kb(x)
+    yv = y.t() if y_out is None else y
+    qgemv.dispatch(yv, vx.QWeight(w, qtype, M, K), xv, x_int8=x_int8)
+    torch.cuda.synchronize()
+    ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
+    return yv.cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 8, 16, 21])
+@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536)])
+def test_gemv_parity_small(qgemv, qtype, B, M, K):
+    if K % O.QTYPE_INFO[qtype][0]:
+        pytest.skip("K not a multiple of the block size")
+    note(f"gemv {QN[qtype]} M={M} K={K} B={B}")
+    got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=M + K + B)
+    assert_close(got, ref, what=f"{QN[qtype]} {M}x{K} b{B}")
+
+
+# BASELINE.json configs at full size.
+FULL = [
+    (vx.VX_Q8_0, 4096, 4096, 1), (vx.VX_Q8_0, 4096, 4096, 8),
+    (vx.VX_Q4_0, 11008, 4096, 1), (vx.VX_Q4_0, 11008, 4096, 4), (vx.VX_Q4_0, 11008, 4096, 8),
+    (vx.VX_Q4_0, 4096, 11008, 1),
+    (vx.VX_Q4_K, 14336, 4096, 1), (vx.VX_Q4_K, 14336, 4096, 16),
+    (vx.VX_Q4_K, 32000, 4096, 1), (vx.VX_Q4_K, 32000, 4096, 16),
+]
+
+
+@pytest.mark.parametrize("qtype,M,K,B", FULL, ids=[f"{QN[q]}-{m}x{k}-b{b}" for q, m, k, b in FULL])
+def test_gemv_parity_configs(qgemv, qtype, M, K, B):
+    note(f"gemv config {QN[qtype]} {M}x{K} b{B}")
+    got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=7)
+    assert_close(got, ref, what=f"{QN[qtype]} {M}x{K} b{B}")
+    if B == 1:
+        note(f"gemv config int8-x {QN[qtype]} {M}x{K}")
+        got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=8, x_int8=True)
+        assert_close(got, ref, what=f"int8-x {QN[qtype]} {M}x{K}")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536), (33, 64 * 300)])
+def test_gemv_int8x_path_small(qgemv, qtype, M, K):
+    if K % O.QTYPE_INFO[qtype][0]:
+        pytest.skip("K not a multiple of the block size")
+    note(f"gemv int8-x {QN[qtype]} M={M} K={K}")
+    got, ref = _run_gemv(qgemv, qtype, M, K, 1, seed=M + K, x_int8=True)
+    assert_close(got, ref, what="int8-x path")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_gemv_x_edge_values(qgemv, qtype):
+    """Both batch-1 paths with x blocks that are all zero, tiny, huge, or one
+    large outlier among small values; K spanning several LDS chunks."""
+    M, K = 40, 64 * 300
+    note(f"gemv i8 edge x {QN[qtype]}")
+    w = S.quant_weights(qtype, M, K, seed=3, device=DEV)
+    x = S.activations(1, K, seed=4, device=DEV)
+    x[0, 0:32] = 0.0
+    x[0, 32:64] *= 1e-30
+    x[0, 64:96] *= 1e30
+    x[0, 96:128] *= 1e-3
+    x[0, 100] = 50.0
+    y = torch.full((M,), float("nan"), device=DEV)
+    ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())[:, 0]
+    for x_int8 in (False, True):
+        y.fill_(float("nan"))
+        qgemv.dispatch(y, vx.QWeight(w, qtype, M, K), x[0], x_int8=x_int8)
+        torch.cuda.synchronize()
+        assert_close(y.cpu().numpy(), ref, what=f"x_int8={x_int8}")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_gemv_generic_paths(qgemv, qtype):
+    """Odd block counts, padded (unaligned) row strides and strided x / y
+    take the byte-level fallback or the scalar x staging."""
+    qk, bb = O.QTYPE_INFO[qtype]
+    K = 3 * qk if qtype != vx.VX_Q4_K else 512
+    M, B = 45, 3
+    note(f"gemv generic {QN[qtype]} K={K}")
+    w = S.quant_weights(qtype, M, K, seed=5).numpy()
+    rb = w.shape[1]
+    padded = np.zeros((M, rb + 2), dtype=np.uint8)  # row stride not a multiple of 4
+    padded[:, :rb] = w
+    wd = torch.from_numpy(padded).to(DEV)
+    x = S.activations(B, K, seed=6, device=DEV)
+    xbig = torch.zeros((K, 2 * B), device=DEV)
+    xbig[:, ::2] = x.t()
+    y = torch.full((M, 2 * B), float("nan"), device=DEV)
+    qgemv.dispatch(y[:, 1::2], vx.QWeight(wd, qtype, M, K, row_stride=rb + 2), xbig[:, ::2])
+    torch.cuda.synchronize()
+    ref = O.gemv_q_f64(qtype, w, M, K, x.cpu().numpy())
+    assert_close(y[:, 1::2].cpu().numpy(), ref, what="generic")
+    assert torch.isnan(y[:, 0::2]).all()
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_gemv_strided_x_fast_weights(qgemv, qtype):
+    """Aligned weights with x not contiguous along K (scalar staging)."""
+    M, K, B = 64, 4096, 2
+    note(f"gemv strided-x {QN[qtype]}")
+    got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=9, x_kb=lambda x: x.t().contiguous())
+    assert_close(got, ref)
+    w = S.quant_weights(qtype, M, K, seed=19, device=DEV)
+    x = S.activations(B, K, seed=20, device=DEV)
+    xkb = torch.empty((K, 3 * B), device=DEV)
+    xkb[:, ::3] = x.t()
+    y = torch.full((M, B), float("nan"), device=DEV)
+    qgemv.dispatch(y, vx.QWeight(w, qtype, M, K), xkb[:, ::3])
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy()))
+
+
+def test_gemv_shape_errors(qgemv):
+    M, K = 8, 64
+    w = vx.QWeight(torch.zeros((M, K // 32 * 18), dtype=torch.uint8, device=DEV), vx.VX_Q4_0, M, K)
+    with pytest.raises(vx.VortxError, match="VX_ERR_SHAPE"):
+        qgemv.dispatch(torch.zeros(M + 1, device=DEV), w, torch.zeros(K, device=DEV))
+    with pytest.raises(vx.VortxError, match="VX_ERR_SHAPE"):
+        qgemv.dispatch(torch.zeros(M, device=DEV), w, torch.zeros(K + 1, device=DEV))
+    bad = vx.QWeight(w.data, vx.VX_Q4_0, M, K)
+    bad.qtype = 3  # not a supported GGML type
+    with pytest.raises(vx.VortxError, match="VX_ERR_INVALID"):
+        qgemv.dispatch(torch.zeros(M, device=DEV), bad, torch.zeros(K, device=DEV))

@@ -1,0 +1,221 @@
+"""CPU tests that pin the oracle (oracle/vx_oracle.c) before it is trusted.
+
+* f16 -> f32: all 65536 bit patterns against numpy's binary16 conversion.
+* Block decode: the hand-built known-answer blocks of tests/golden, plus
+  invariants a plausible mistake breaks: one-hot nibble positions, exact
+  linearity in d, the Q4_0 / Q8_0 identity (a Q4_0 block equals the Q8_0
+  block holding nibble - 8 with the same d), and Q4_K scale unpacking over
+  every 6-bit value.
+* GEMM: the reference-order f32 restatement and the f64 contraction against
+  numpy (BLAS) float64 matmul, integer-exact products, closed forms (K = 0,
+  identity, outer product K = 1) and strided / transposed views.
+* GEMV: the f64 oracle against numpy's float64 product of the decoded
+  matrix; the CPU-baseline kernels against the oracle.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_f16_exhaustive_matches_numpy():
+    bits = np.arange(65536, dtype=np.uint16)
+    got = O.f16_to_f32(bits)
+    exp = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(exp)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), exp[~nan].view(np.uint32))
+
+
+def _golden():
+    with open(os.path.join(GOLDEN, "quant_known_answers.json")) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _golden(), ids=lambda c: c["name"])
+def test_decode_known_answers(case):
+    blk = np.frombuffer(bytes.fromhex(case["block"]), np.uint8)[None, :]
+    qk, bb = O.QTYPE_INFO[case["qtype"]]
+    assert blk.shape[1] == bb
+    got = O.dequant(case["qtype"], blk, 1, qk)[0]
+    exp = np.array(case["expected"], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), np.nonzero(got != exp)
+
+
+def test_q4k_scale_unpack_matches_golden():
+    case = [c for c in _golden() if c["name"] == "q4k_highbits"][0]
+    sc12 = bytes.fromhex(case["block"])[4:16]
+    for s in range(8):
+        assert O.q4k_scale_min(sc12, s) == (case["scales"][s], case["mins"][s])
+
+
+def _q4k_pack(sc, m):
+    b = [0] * 12
+    for s in range(4):
+        b[s] = (sc[s] & 63) | ((sc[s + 4] >> 4) << 6)
+        b[s + 4] = (m[s] & 63) | ((m[s + 4] >> 4) << 6)
+        b[s + 8] = (sc[s + 4] & 15) | ((m[s + 4] & 15) << 4)
+    return bytes(b)
+
+
+def test_q4k_scale_unpack_every_value():
+    rng = np.random.default_rng(0)
+    for v in range(64):
+        sc = list(rng.integers(0, 64, 8))
+        m = list(rng.integers(0, 64, 8))
+        s = v % 8
+        sc[s], m[(s + 3) % 8] = v, 63 - v
+        packed = _q4k_pack(sc, m)
+        for t in range(8):
+            assert O.q4k_scale_min(packed, t) == (sc[t], m[t])
+
+
+def test_q4_0_one_hot_positions():
+    """A single non-zero (q - 8) lands at element j (low nibble) or j + 16."""
+    for j in range(16):
+        for hi in (False, True):
+            qs = bytearray([0x88] * 16)
+            qs[j] = (0x8F if not hi else 0xF8)
+            blk = np.frombuffer(bytes.fromhex("003c") + bytes(qs), np.uint8)[None, :]
+            got = O.dequant(O.Q4_0, blk, 1, 32)[0]
+            nz = np.nonzero(got)[0]
+            assert list(nz) == [j + 16 * hi] and got[nz[0]] == 7.0
+
+
+def test_q4k_one_hot_positions():
+    """Byte l of chunk c: low nibble -> element 64c + l, high -> 64c + 32 + l."""
+    sc = [1] * 8
+    m = [0] * 8
+    head = bytes.fromhex("003c") + bytes.fromhex("0000") + _q4k_pack(sc, m)
+    for c in range(4):
+        for l in (0, 7, 31):
+            for hi in (False, True):
+                qs = bytearray(128)
+                qs[32 * c + l] = 0x50 if hi else 0x05
+                blk = np.frombuffer(head + bytes(qs), np.uint8)[None, :]
+                got = O.dequant(O.Q4_K, blk, 1, 256)[0]
+                nz = np.nonzero(got)[0]
+                assert list(nz) == [64 * c + 32 * hi + l] and got[nz[0]] == 5.0
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K])
+def test_decode_linear_in_d(qtype):
+    """Doubling d (and dmin) doubles every decoded weight exactly."""
+    qk, bb = O.QTYPE_INFO[qtype]
+    rng = np.random.default_rng(qtype)
+    w = rng.integers(0, 256, size=(16, 4 * bb), dtype=np.uint8)
+    blocks = w.reshape(16, 4, bb)
+    d = np.abs(rng.standard_normal((16, 4, 2 if qtype == O.Q4_K else 1))).astype(np.float16) + np.float16(0.01)
+    blocks[..., 0:d.shape[-1] * 2] = d.view(np.uint8).reshape(16, 4, -1)
+    base = O.dequant(qtype, blocks.reshape(16, -1), 16, 4 * qk)
+    blocks2 = blocks.copy()
+    blocks2[..., 0:d.shape[-1] * 2] = (d * np.float16(2)).view(np.uint8).reshape(16, 4, -1)
+    dbl = O.dequant(qtype, blocks2.reshape(16, -1), 16, 4 * qk)
+    assert np.array_equal(dbl, 2 * base)
+
+
+def test_q4_0_equals_q8_0_with_centered_nibbles():
+    rng = np.random.default_rng(5)
+    nib = rng.integers(0, 16, size=(8, 32))
+    d = np.abs(rng.standard_normal(8)).astype(np.float16)
+    q40 = np.zeros((8, 18), np.uint8)
+    q80 = np.zeros((8, 34), np.uint8)
+    q40[:, 0:2] = d.view(np.uint8).reshape(8, 2)
+    q80[:, 0:2] = d.view(np.uint8).reshape(8, 2)
+    q40[:, 2:] = nib[:, :16] | (nib[:, 16:] << 4)
+    q80[:, 2:] = (nib - 8).astype(np.int8).view(np.uint8)
+    assert np.array_equal(O.dequant(O.Q4_0, q40, 8, 32), O.dequant(O.Q8_0, q80, 8, 32))
+
+
+# ------------------------------------------------------------------ gemm
+@pytest.mark.parametrize("M,N,K", [(67, 33, 17), (1, 1, 1), (64, 64, 64), (5, 130, 257)])
+def test_gemm_oracles_vs_numpy(M, N, K):
+    rng = np.random.default_rng(M * N * K)
+    a = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    b = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    np.testing.assert_allclose(O.gemm_f64(a, b)[0, 0], ref, rtol=1e-12, atol=1e-12)
+    got = O.gemm_ref_f32(a, b)
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max()) * K ** 0.5
+
+
+def test_gemm_ref_order_is_sequential_f32():
+    """The restatement accumulates k = 0..K-1 in f32 with one rounding per op."""
+    rng = np.random.default_rng(9)
+    a = rng.uniform(-1, 1, (3, 50)).astype(np.float32)
+    b = rng.uniform(-1, 1, (50, 4)).astype(np.float32)
+    exp = np.zeros((3, 4), np.float32)
+    for i in range(3):
+        for j in range(4):
+            s = np.float32(0)
+            for k in range(50):
+                s = np.float32(s + np.float32(a[i, k] * b[k, j]))
+            exp[i, j] = s
+    assert np.array_equal(O.gemm_ref_f32(a, b).view(np.uint32), exp.view(np.uint32))
+
+
+def test_gemm_integer_golden():
+    with open(os.path.join(GOLDEN, "gemm_int_small.json")) as f:
+        g = json.load(f)
+    a = np.array(g["a"], np.float32)
+    b = np.array(g["b"], np.float32)
+    c = np.array(g["c"], np.float32)
+    assert np.array_equal(O.gemm_ref_f32(a, b), c)
+    assert np.array_equal(O.gemm_f64(a, b)[0, 0], c.astype(np.float64))
+
+
+def test_gemm_closed_forms():
+    rng = np.random.default_rng(2)
+    b = rng.uniform(-1, 1, (6, 5)).astype(np.float32)
+    assert np.array_equal(O.gemm_ref_f32(np.eye(6, dtype=np.float32), b), b)
+    a0 = np.zeros((4, 0), np.float32)
+    b0 = np.zeros((0, 3), np.float32)
+    assert np.array_equal(O.gemm_ref_f32(a0, b0), np.zeros((4, 3), np.float32))
+    u = rng.uniform(-1, 1, (7, 1)).astype(np.float32)
+    v = rng.uniform(-1, 1, (1, 9)).astype(np.float32)
+    assert np.array_equal(O.gemm_ref_f32(u, v), (u * v).astype(np.float32))
+
+
+def test_gemm_strided_and_batched_views():
+    rng = np.random.default_rng(4)
+    A = rng.uniform(-1, 1, (2, 3, 40, 30)).astype(np.float32)
+    Bt = rng.uniform(-1, 1, (2, 3, 20, 30)).astype(np.float32)
+    b = Bt.transpose(0, 1, 3, 2)  # transposed view, no copy
+    ref = np.einsum("ncik,nckj->ncij", A.astype(np.float64), b.astype(np.float64))
+    np.testing.assert_allclose(O.gemm_f64(A, b), ref, rtol=1e-12)
+    np.testing.assert_allclose(O.gemm_ref_f32(A, b), ref, rtol=1e-4, atol=1e-5)
+    a_str = A[0, 0, ::2, ::3]
+    np.testing.assert_allclose(O.gemm_f64(a_str, b[0, 0, ::3, :])[0, 0],
+                               a_str.astype(np.float64) @ b[0, 0, ::3, :].astype(np.float64), rtol=1e-12)
+
+
+def test_cpu_baseline_tiled_matches_reference_order():
+    """The OpenMP restatement of gemm_tiled keeps the k order: bit-exact."""
+    rng = np.random.default_rng(6)
+    a = rng.uniform(-1, 1, (100, 70)).astype(np.float32)
+    b = rng.uniform(-1, 1, (70, 90)).astype(np.float32)
+    assert np.array_equal(O.gemm_tiled_f32_omp(a, b, 2).view(np.uint32), O.gemm_ref_f32(a, b).view(np.uint32))
+
+
+# ------------------------------------------------------------------ gemv
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K])
+def test_gemv_oracle_vs_numpy(qtype):
+    M, K, B = 37, 512, 3
+    rng = np.random.default_rng(qtype)
+    w = rng.integers(0, 256, size=(M, O.row_bytes(qtype, K)), dtype=np.uint8)
+    qk, bb = O.QTYPE_INFO[qtype]
+    blocks = w.reshape(M, K // qk, bb)
+    nd = 2 if qtype == O.Q4_K else 1  # d (and dmin) kept in a realistic range
+    blocks[..., 0:2 * nd] = (np.abs(rng.standard_normal((M, K // qk, nd))) * 0.01).astype(np.float16).view(
+        np.uint8).reshape(M, K // qk, 2 * nd)
+    x = rng.standard_normal((B, K)).astype(np.float32)
+    W = O.dequant(qtype, w, M, K).astype(np.float64)
+    ref = W @ x.T.astype(np.float64)
+    np.testing.assert_allclose(O.gemv_q_f64(qtype, w, M, K, x), ref, rtol=1e-12, atol=1e-12)
+    got = O.gemv_q_f32_omp(qtype, w, M, K, x, 2)
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()

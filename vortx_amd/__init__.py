@@ -1,0 +1,234 @@
+"""vortx_amd — MI355X (gfx950) linalg hot path of vortx behind a C ABI.
+
+Python-side mirror of the reference interface for this path:
+
+* :class:`TensorLayout` — vortx's view algebra (src/shapes.rs:51-530),
+  computed by the native library;
+* :class:`Gemm` — ``Gemm::dispatch`` / ``dispatch_naive`` / ``dispatch_tiled``
+  (src/linalg/gemm.rs:47-305) on f32 views: out = lhs * rhs;
+* :class:`QuantGemv` — block-quantized GEMV y = W x (Q8_0, Q4_0, Q4_K) and
+  dequantize, which the reference does not have.
+
+A view is either a torch tensor on the GPU (its sizes, strides and storage
+offset become the layout) or a ``(buffer, TensorLayout)`` pair, exactly like
+vortx's ``TensorRef { layout, buffer }``. torch only provides device memory
+and streams; every launch goes through libvortx_hip.so, and there is no CPU
+fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+from . import _ffi
+from ._ffi import (NONE_STRIDE, ROUTE_EMPTY, ROUTE_GEMV, ROUTE_NAIVE, ROUTE_TILED, VX_Q4_0, VX_Q4_K, VX_Q8_0,
+                   VortxError, check, lib)
+
+__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
+           "ROUTE_NAIVE", "ROUTE_TILED", "ROUTE_GEMV", "ROUTE_EMPTY", "qtype_info", "lib"]
+
+# Load eagerly: a missing library must fail at import, not at first call.
+lib()
+
+
+# ---------------------------------------------------------------- layout
+@dataclass(frozen=True)
+class TensorLayout:
+    """vortx's TensorLayout (src/shapes.rs:51-60): element sizes/strides, rank <= 4."""
+    size: tuple
+    stride: tuple
+    rank: int
+    offset: int = 0
+
+    def _c(self) -> _ffi.VxLayout:
+        l = _ffi.VxLayout()
+        for i in range(4):
+            l.size[i] = self.size[i] if i < len(self.size) else 1
+            l.stride[i] = self.stride[i] if i < len(self.stride) else 1
+        l.rank = self.rank
+        l.offset = self.offset
+        return l
+
+    @staticmethod
+    def _py(l: _ffi.VxLayout) -> "TensorLayout":
+        return TensorLayout(tuple(l.size), tuple(l.stride), l.rank, l.offset)
+
+    @staticmethod
+    def contiguous(size) -> "TensorLayout":
+        arr = (C.c_uint32 * max(1, len(size)))(*size)
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_contiguous(arr, len(size), C.byref(out)))
+        return TensorLayout._py(out)
+
+    def dims(self) -> tuple:
+        return self.size[:self.rank]
+
+    def canonicalize(self) -> "TensorLayout":
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_canonicalize(C.byref(self._c()), C.byref(out)))
+        return TensorLayout._py(out)
+
+    def transpose(self, a: int, b: int) -> "TensorLayout":
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_transpose(C.byref(self._c()), a, b, C.byref(out)))
+        return TensorLayout._py(out)
+
+    def broadcast(self, other: "TensorLayout"):
+        """(self', other') or None when incompatible (src/shapes.rs:346-391)."""
+        a, b = _ffi.VxLayout(), _ffi.VxLayout()
+        s = lib().vx_layout_broadcast(C.byref(self._c()), C.byref(other._c()), C.byref(a), C.byref(b))
+        if s == _ffi.VX_ERR_SHAPE:
+            return None
+        check(s)
+        return TensorLayout._py(a), TensorLayout._py(b)
+
+    def view(self, offset: int, shape, stride=()) -> "TensorLayout":
+        sh = (C.c_uint32 * max(1, len(shape)))(*shape)
+        st = (C.c_uint32 * max(1, len(stride)))(*[NONE_STRIDE if s is None else s for s in stride])
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_view(C.byref(self._c()), offset, sh, len(shape), st, len(stride), C.byref(out)))
+        return TensorLayout._py(out)
+
+    def narrow(self, axis: int, first: int, count: int) -> "TensorLayout":
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_narrow(C.byref(self._c()), axis, first, count, C.byref(out)))
+        return TensorLayout._py(out)
+
+    def unsqueeze(self, axis: int) -> "TensorLayout":
+        out = _ffi.VxLayout()
+        check(lib().vx_layout_unsqueeze(C.byref(self._c()), axis, C.byref(out)))
+        return TensorLayout._py(out)
+
+    def is_contiguous(self) -> bool:
+        return bool(lib().vx_layout_is_contiguous(C.byref(self._c())))
+
+
+def _view_of(v, mutable: bool):
+    """torch tensor or (buffer, TensorLayout) -> VxCView / VxMView."""
+    import torch
+    if isinstance(v, tuple):
+        buf, layout = v
+        if not (isinstance(buf, torch.Tensor) and buf.dtype == torch.float32 and buf.is_cuda):
+            raise TypeError("view buffer must be a float32 tensor on the GPU")
+        base = buf.data_ptr()
+    else:
+        if not (isinstance(v, torch.Tensor) and v.dtype == torch.float32 and v.is_cuda):
+            raise TypeError("views must be float32 tensors on the GPU")
+        if v.dim() > 4:
+            raise VortxError(_ffi.VX_ERR_UNSUPPORTED, "tensors of ranks > 4 not supported")
+        if any(s < 0 for s in v.stride()):
+            raise VortxError(_ffi.VX_ERR_UNSUPPORTED, "negative strides")
+        base = v.untyped_storage().data_ptr()
+        layout = TensorLayout(tuple(v.shape), tuple(v.stride()), v.dim(), v.storage_offset())
+    view = (_ffi.VxMView if mutable else _ffi.VxCView)()
+    view.base = base
+    view.layout = layout._c()
+    return view
+
+
+def _stream(stream) -> int:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+# ------------------------------------------------------------------ gemm
+class _Context:
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().vx_init(device, C.byref(h)))
+        self._h = h
+        self.device = device
+        n = C.c_int()
+        check(lib().vx_device_info(h, None, C.byref(n)))
+        self.num_cus = n.value
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().vx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Gemm(_Context):
+    """f32 GEMM on tensor views: out = lhs * rhs (src/linalg/gemm.rs:34-321).
+
+    ``dispatch`` validates like the reference (a shape mismatch raises
+    VortxError(VX_ERR_SHAPE) where vortx panics) and routes: naive kernel when
+    M < 32 and N < 32, f32 GEMV when N == 1, MFMA tiled kernel otherwise.
+    """
+
+    def _call(self, fn, out, lhs, rhs, stream):
+        o, l, r = _view_of(out, True), _view_of(lhs, False), _view_of(rhs, False)
+        check(fn(self._h, _stream(stream), C.byref(o), C.byref(l), C.byref(r)))
+
+    def dispatch(self, out, lhs, rhs, stream=None) -> None:
+        self._call(lib().vx_gemm_f32, out, lhs, rhs, stream)
+
+    def dispatch_naive(self, out, lhs, rhs, stream=None) -> None:
+        self._call(lib().vx_gemm_f32_naive, out, lhs, rhs, stream)
+
+    def dispatch_tiled(self, out, lhs, rhs, stream=None) -> None:
+        self._call(lib().vx_gemm_f32_tiled, out, lhs, rhs, stream)
+
+    @staticmethod
+    def route(out, lhs, rhs) -> int:
+        o, l, r = _view_of(out, True), _view_of(lhs, False), _view_of(rhs, False)
+        rt = C.c_int()
+        check(lib().vx_gemm_f32_route(C.byref(o), C.byref(l), C.byref(r), C.byref(rt)))
+        return rt.value
+
+
+# ----------------------------------------------------------------- quant
+def qtype_info(qtype: int) -> tuple:
+    """(weights per block, bytes per block)."""
+    qk, bb = C.c_uint32(), C.c_uint32()
+    check(lib().vx_qtype_info(qtype, C.byref(qk), C.byref(bb)))
+    return qk.value, bb.value
+
+
+@dataclass
+class QWeight:
+    """Row-major block-quantized matrix [rows, cols] in a uint8 GPU tensor."""
+    data: object  # torch.uint8 tensor on the GPU, >= rows * row_stride bytes
+    qtype: int
+    rows: int
+    cols: int
+    row_stride: int = 0
+
+    def __post_init__(self):
+        qk, bb = qtype_info(self.qtype)
+        if self.row_stride == 0:
+            self.row_stride = self.cols // qk * bb
+
+    def _c(self) -> _ffi.VxQWeight:
+        w = _ffi.VxQWeight()
+        w.base = self.data.data_ptr()
+        w.qtype = self.qtype
+        w.rows = self.rows
+        w.cols = self.cols
+        w.reserved = 0
+        w.row_stride_bytes = self.row_stride
+        return w
+
+
+class QuantGemv(_Context):
+    """y = W x for GGML Q8_0 / Q4_0 / Q4_K weights, f32 accumulate."""
+
+    def dispatch(self, y, w: QWeight, x, stream=None, x_int8: bool = False) -> None:
+        """y = W x with f32 x and f32 accumulation. ``x_int8=True`` (batch 1)
+        selects the integer-dot path (x split into two int8 levels per
+        32-block, exact int32 block sums)."""
+        yv, xv, wc = _view_of(y, True), _view_of(x, False), w._c()
+        flags = _ffi.VX_GEMV_X_INT8 if x_int8 else 0
+        check(lib().vx_gemv_q_ex(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags))
+
+    def dequantize(self, out, w: QWeight, stream=None) -> None:
+        ov, wc = _view_of(out, True), w._c()
+        check(lib().vx_dequantize(self._h, _stream(stream), C.byref(ov), C.byref(wc)))

@@ -1,0 +1,95 @@
+"""ctypes binding of libvortx_hip.so (the C ABI in include/vortx_hip.h).
+
+The library is loaded from this package directory only; there is no
+fallback implementation: if it is missing, importing ``vortx_amd`` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libvortx_hip.so")
+
+VX_OK, VX_ERR_SHAPE, VX_ERR_UNSUPPORTED, VX_ERR_INVALID, VX_ERR_HIP, VX_ERR_NO_CODE_OBJECT = range(6)
+VX_Q4_0, VX_Q8_0, VX_Q4_K = 2, 8, 12
+ROUTE_NAIVE, ROUTE_TILED, ROUTE_GEMV, ROUTE_EMPTY = range(4)
+NONE_STRIDE = 0xFFFFFFFF
+VX_GEMV_X_INT8 = 1
+
+
+class VxLayout(C.Structure):
+    _fields_ = [("size", C.c_uint32 * 4), ("stride", C.c_uint32 * 4), ("rank", C.c_uint32), ("offset", C.c_uint32)]
+
+
+class VxCView(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("layout", VxLayout)]
+
+
+class VxMView(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("layout", VxLayout)]
+
+
+class VxQWeight(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("qtype", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+                ("reserved", C.c_uint32), ("row_stride_bytes", C.c_uint64)]
+
+
+# (name, restype, argtypes) for every exported entry point.
+_P = C.POINTER
+SIGNATURES = [
+    ("vx_init", C.c_int, [C.c_int, _P(C.c_void_p)]),
+    ("vx_destroy", C.c_int, [C.c_void_p]),
+    ("vx_device_info", C.c_int, [C.c_void_p, _P(C.c_int), _P(C.c_int)]),
+    ("vx_gemm_f32", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
+    ("vx_gemm_f32_naive", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
+    ("vx_gemm_f32_tiled", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
+    ("vx_gemm_f32_route", C.c_int, [_P(VxMView), _P(VxCView), _P(VxCView), _P(C.c_int)]),
+    ("vx_gemv_q", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView)]),
+    ("vx_gemv_q_ex", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView), C.c_uint32]),
+    ("vx_dequantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight)]),
+    ("vx_qtype_info", C.c_int, [C.c_uint32, _P(C.c_uint32), _P(C.c_uint32)]),
+    ("vx_layout_contiguous", C.c_int, [_P(C.c_uint32), C.c_uint32, _P(VxLayout)]),
+    ("vx_layout_canonicalize", C.c_int, [_P(VxLayout), _P(VxLayout)]),
+    ("vx_layout_transpose", C.c_int, [_P(VxLayout), C.c_uint32, C.c_uint32, _P(VxLayout)]),
+    ("vx_layout_broadcast", C.c_int, [_P(VxLayout), _P(VxLayout), _P(VxLayout), _P(VxLayout)]),
+    ("vx_layout_view", C.c_int, [_P(VxLayout), C.c_uint32, _P(C.c_uint32), C.c_uint32, _P(C.c_uint32),
+                                 C.c_uint32, _P(VxLayout)]),
+    ("vx_layout_narrow", C.c_int, [_P(VxLayout), C.c_uint32, C.c_uint32, C.c_uint32, _P(VxLayout)]),
+    ("vx_layout_unsqueeze", C.c_int, [_P(VxLayout), C.c_uint32, _P(VxLayout)]),
+    ("vx_layout_is_contiguous", C.c_int, [_P(VxLayout)]),
+    ("vx_status_string", C.c_char_p, [C.c_int]),
+    ("vx_last_error_message", C.c_char_p, []),
+    ("vx_last_hip_error", C.c_int, []),
+]
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "(there is no non-HIP fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+class VortxError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        name = lib().vx_status_string(status).decode()
+        super().__init__(f"{name}: {message}")
+
+
+def check(status: int) -> None:
+    if status != VX_OK:
+        raise VortxError(status, lib().vx_last_error_message().decode())

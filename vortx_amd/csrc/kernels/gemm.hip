@@ -1,0 +1,272 @@
+// gemm.hip — f32 GEMM kernels for gfx950 on canonical [n, c, rows, cols]
+// views (any strides; batch dims n, c folded into grid z).
+//
+//  vx_gemm_naive   one thread per output, sequential-k f32 sum with one
+//                  rounding per multiply and per add: the summation order of
+//                  the reference's gemm_naive / gemm_tiled
+//                  (vortx-shaders/src/linalg/gemm.rs:84-171, 225-235).
+//  vx_gemm_mfma_*  128x128 output tile per workgroup (4 wave64 in 2x2, each
+//                  64x64 = 2x2 v_mfma_f32_32x32x2f32 accumulators), K staged
+//                  16 at a time through double-buffered LDS (k-major, one
+//                  barrier per stage). Operand loads are 128-bit along the
+//                  contiguous dimension of each operand; edge tiles are
+//                  zero-filled like the reference (gemm.rs:102-106,121-125).
+//  vx_gemv_f32     the N == 1 case: one wave per output row, 128-bit loads
+//                  along K, xor-shuffle reduction.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../vx_kargs.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define TBM 128
+#define TBN 128
+#define TBK 16
+#define LDS_PAD 4
+#define LDA_S (TBM + LDS_PAD)
+#define LDB_S (TBN + LDS_PAD)
+
+// Operand access modes (chosen on the host from strides and alignment).
+#define MODE_KC 0  // contiguous along K, rows 16-byte aligned
+#define MODE_XC 1  // contiguous along M (for A) / N (for B), 16-byte aligned
+#define MODE_GEN 2 // anything else: scalar loads
+
+// ---------------------------------------------------------------- naive
+extern "C" __global__ __launch_bounds__(64) void vx_gemm_naive(vx_gemm_args p) {
+    const uint32_t j = blockIdx.x * 64u + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const uint32_t z = blockIdx.z;
+    if (j >= p.N) return;
+    const uint32_t bn = z / p.batch_c, bc = z % p.batch_c;
+    const float* a = p.a + bn * p.as[0] + bc * p.as[1] + (int64_t)i * p.as[2];
+    const float* b = p.b + bn * p.bs[0] + bc * p.bs[1] + (int64_t)j * p.bs[3];
+    float sum = 0.f;
+    for (uint32_t k = 0; k < p.K; ++k) {
+        // One rounding per multiply and per add (no FMA contraction).
+#pragma clang fp contract(off)
+        sum = sum + a[(int64_t)k * p.as[3]] * b[(int64_t)k * p.bs[2]];
+    }
+    p.c[bn * p.cs[0] + bc * p.cs[1] + (int64_t)i * p.cs[2] + (int64_t)j * p.cs[3]] = sum;
+}
+
+// ----------------------------------------------------------------- mfma
+// Global -> register fragment of one TBK slice of an operand tile.
+// "x" is the non-K dimension of the operand (M for A, N for B); sx/sk the
+// element strides along x and k; X the operand's extent along x.
+template <int MODE>
+struct vx_frag {
+    float v[8];
+};
+
+template <int MODE>
+__device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base, int64_t sx, int64_t sk,
+                                             uint32_t x0, uint32_t X, uint32_t k0, uint32_t K) {
+    const uint32_t t = threadIdx.x;
+    if constexpr (MODE == MODE_KC) {
+        // 128 x-rows of 4 float4 along k: element (x = f>>2, k = 4(f&3)).
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const uint32_t x = x0 + (fi >> 2), k = k0 + 4u * (fi & 3u);
+            const float* p = base + (int64_t)x * sx + k;
+            if (x < X && k + 3 < K) {
+                const f32x4 q = *(const f32x4*)p;
+                f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f.v[4 * i + e] = (x < X && k + e < K) ? p[e] : 0.f;
+            }
+        }
+    } else if constexpr (MODE == MODE_XC) {
+        // 16 k-rows of 32 float4 along x: element (k = f>>5, x = 4(f&31)).
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const uint32_t k = k0 + (fi >> 5), x = x0 + 4u * (fi & 31u);
+            const float* p = base + (int64_t)k * sk + x;
+            if (k < K && x + 3 < X) {
+                const f32x4 q = *(const f32x4*)p;
+                f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) f.v[4 * i + e] = (k < K && x + e < X) ? p[e] : 0.f;
+            }
+        }
+    } else {
+        // scalar: element (k = f>>7, x = f&127), f = t + 256 i.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const uint32_t k = k0 + (fi >> 7), x = x0 + (fi & 127u);
+            f.v[i] = (k < K && x < X) ? base[(int64_t)k * sk + (int64_t)x * sx] : 0.f;
+        }
+    }
+}
+
+// Register fragment -> LDS tile S[k][x] (row pitch LD).
+template <int MODE, int LD>
+__device__ __forceinline__ void vx_store_frag(const vx_frag<MODE>& f, float* S) {
+    const uint32_t t = threadIdx.x;
+    if constexpr (MODE == MODE_KC) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const uint32_t x = fi >> 2, k = 4u * (fi & 3u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S[(k + e) * LD + x] = f.v[4 * i + e];
+        }
+    } else if constexpr (MODE == MODE_XC) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const uint32_t k = fi >> 5, x = 4u * (fi & 31u);
+            *(f32x4*)(S + k * LD + x) = f32x4{f.v[4 * i], f.v[4 * i + 1], f.v[4 * i + 2], f.v[4 * i + 3]};
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t fi = t + 256u * i;
+            S[(fi >> 7) * LD + (fi & 127u)] = f.v[i];
+        }
+    }
+}
+
+template <int AMODE, int BMODE>
+__device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
+    __shared__ float As[2][TBK * LDA_S];
+    __shared__ float Bs[2][TBK * LDB_S];
+
+    // Tile order: consecutive workgroup ids land on different XCDs (round
+    // robin over 8), so ids are first regrouped per XCD, then walked in
+    // groups of 8 tile-rows so an XCD's resident tiles share A and B panels
+    // in its L2.
+    const uint32_t nt = p.tiles_m * p.tiles_n;
+    uint32_t bid = blockIdx.x;
+    if ((nt & 7u) == 0) bid = (bid & 7u) * (nt >> 3) + (bid >> 3);
+    const uint32_t group = 8u * p.tiles_n;
+    const uint32_t first_m = (bid / group) * 8u;
+    const uint32_t gsize = min(p.tiles_m - first_m, 8u);
+    const uint32_t tm = first_m + (bid % group) % gsize;
+    const uint32_t tn = (bid % group) / gsize;
+    const uint32_t m0 = tm * TBM, n0 = tn * TBN;
+
+    const uint32_t z = blockIdx.z;
+    const uint32_t bn = z / p.batch_c, bc = z % p.batch_c;
+    const float* A = p.a + bn * p.as[0] + bc * p.as[1];
+    const float* B = p.b + bn * p.bs[0] + bc * p.bs[1];
+    float* Cp = p.c + bn * p.cs[0] + bc * p.cs[1];
+
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t l32 = lane & 31u, lk = lane >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    vx_frag<AMODE> fa;
+    vx_frag<BMODE> fb;
+    const uint32_t nk = (p.K + TBK - 1) / TBK;
+    if (nk) {
+        vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
+        vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
+        vx_store_frag<AMODE, LDA_S>(fa, As[0]);
+        vx_store_frag<BMODE, LDB_S>(fb, Bs[0]);
+        __syncthreads();
+    }
+    for (uint32_t kt = 0; kt < nk; ++kt) {
+        const uint32_t cur = kt & 1u;
+        const bool more = kt + 1 < nk;
+        if (more) {
+            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
+            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
+        }
+        const float* as = As[cur] + wm * 64u + l32;
+        const float* bs = Bs[cur] + wn * 64u + l32;
+#pragma unroll
+        for (int ks = 0; ks < TBK / 2; ++ks) {
+            const uint32_t kk = 2u * ks + lk;
+            const float a0 = as[kk * LDA_S], a1 = as[kk * LDA_S + 32];
+            const float b0 = bs[kk * LDB_S], b1 = bs[kk * LDB_S + 32];
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+        }
+        if (more) {
+            vx_store_frag<AMODE, LDA_S>(fa, As[cur ^ 1u]);
+            vx_store_frag<BMODE, LDB_S>(fb, Bs[cur ^ 1u]);
+        }
+        __syncthreads();
+    }
+
+    // D layout of v_mfma_f32_32x32x2f32: register v of lane l holds
+    // row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the 32x32 tile.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t col = n0 + wn * 64u + 32u * j + l32;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t row = m0 + wm * 64u + 32u * i + 8u * (v >> 2) + 4u * lk + (v & 3);
+                if (row < p.M && col < p.N) Cp[(int64_t)row * p.cs[2] + (int64_t)col * p.cs[3]] = acc[i][j][v];
+            }
+        }
+}
+
+#define VX_GEMM_MFMA(AM, BM, NAME)                                                                   \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemm_mfma_##NAME(vx_gemm_args p) { \
+        vx_gemm_mfma<AM, BM>(p);                                                                     \
+    }
+// Suffix letters: A mode then B mode; k = contiguous along K,
+// x = contiguous along M / N, g = generic.
+VX_GEMM_MFMA(MODE_KC, MODE_XC, kx)  // row-major A, row-major B
+VX_GEMM_MFMA(MODE_KC, MODE_KC, kk)  // row-major A, B = transposed view of [N, K]
+VX_GEMM_MFMA(MODE_XC, MODE_XC, xx)
+VX_GEMM_MFMA(MODE_XC, MODE_KC, xk)
+VX_GEMM_MFMA(MODE_GEN, MODE_GEN, gg)
+VX_GEMM_MFMA(MODE_KC, MODE_GEN, kg)
+VX_GEMM_MFMA(MODE_GEN, MODE_XC, gx)
+
+// ---------------------------------------------------------------- gemv
+// y[m] = sum_k A[m, k] x[k]; A contiguous along K with 16-byte aligned
+// rows (as_k == 1); x any stride. Grid: (ceil(M/4), batch).
+extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_f32(vx_gemv_f32_args p) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (row >= p.M) return;  // wave-uniform, no barrier below
+    const uint32_t z = blockIdx.y;
+    const uint32_t bn = z / p.batch_c, bc = z % p.batch_c;
+    const float* a = p.a + bn * p.a_bs[0] + bc * p.a_bs[1] + (int64_t)row * p.as_m;
+    const float* x = p.x + bn * p.x_bs[0] + bc * p.x_bs[1];
+    float acc = 0.f;
+    const uint32_t K4 = p.K & ~3u;
+    if (p.xs_k == 1) {
+        for (uint32_t k = 4u * lane; k < K4; k += 256u) {
+            const f32x4 av = *(const f32x4*)(a + k);
+            acc = __builtin_fmaf(av.x, x[k], acc);
+            acc = __builtin_fmaf(av.y, x[k + 1], acc);
+            acc = __builtin_fmaf(av.z, x[k + 2], acc);
+            acc = __builtin_fmaf(av.w, x[k + 3], acc);
+        }
+    } else {
+        for (uint32_t k = 4u * lane; k < K4; k += 256u) {
+            const f32x4 av = *(const f32x4*)(a + k);
+            acc = __builtin_fmaf(av.x, x[(int64_t)k * p.xs_k], acc);
+            acc = __builtin_fmaf(av.y, x[(int64_t)(k + 1) * p.xs_k], acc);
+            acc = __builtin_fmaf(av.z, x[(int64_t)(k + 2) * p.xs_k], acc);
+            acc = __builtin_fmaf(av.w, x[(int64_t)(k + 3) * p.xs_k], acc);
+        }
+    }
+    for (uint32_t k = K4 + lane; k < p.K; k += 64u) acc = __builtin_fmaf(a[k], x[(int64_t)k * p.xs_k], acc);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (lane == 0) p.y[bn * p.y_bs[0] + bc * p.y_bs[1] + (int64_t)row * p.ys_m] = acc;
+}

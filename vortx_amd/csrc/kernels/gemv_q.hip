@@ -1,0 +1,549 @@
+// gemv_q.hip — block-quantized GEMV y = W x and dequantize, for gfx950.
+//
+// Work split (batch 1, the HBM-bound case):
+//   * workgroup = 4 wave64; wave w owns R consecutive rows;
+//   * x (or a chunk of it) is staged once per workgroup in LDS as
+//     [16 float4 slots][unit] with an odd unit pitch, so both the staging
+//     stores and the per-lane ds_read_b128 are bank-conflict free;
+//   * lane l handles unit (64 weights) l of every row in a pass of 64
+//     units: per row it issues 128-bit loads of the unit's bytes (36 B for
+//     Q4_0, 68 B for Q8_0, 48 B for Q4_K) — a wave's loads for one row
+//     cover the row's contiguous bytes, and the R rows' loads are all in
+//     flight before any is consumed;
+//   * the decoded dot uses one byte->float convert and one FMA per
+//     weight; x for the unit stays in 64 VGPRs across the R rows;
+//   * partial sums are reduced across the wave with xor shuffles.
+// Batch > 1 uses the same staging with exact per-weight decode and x read
+// from LDS per 8-weight group; lanes are split into 64/LPR row groups so
+// that NB * chunk fits the LDS budget.
+#include "vx_quant.hpp"
+
+extern __shared__ f32x4 vx_lds_x[];
+
+// x staging. Units [ub, ub + cu) of the NB batch columns of x go to LDS as
+// slot j of unit ul of column b -> vx_lds_x[(b * 16 + j) * upitch + ul].
+// Float4 f of the chunk is (b, ul, j) with j fastest, so consecutive
+// threads read consecutive 16-byte pieces of x. A thread moves up to four
+// float4 per group; all four loads are issued before any store so a group
+// costs one round trip, and the caller issues the first group's loads
+// before its weight loads so the LDS stores wait only for x.
+struct vx_xgroup {
+    f32x4 v[4];
+};
+
+template <int NB, bool XV>
+__device__ __forceinline__ void vx_stage_load(const vx_gemv_args& a, uint32_t ub, uint32_t cu, uint32_t g0,
+                                              vx_xgroup& xg) {
+    const uint32_t per_col = cu * 16u;
+    const uint32_t total = per_col * NB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // Clamped, unconditional loads (no divergent branch between them);
+        // entries past the chunk are loaded but never stored.
+        const uint32_t f = min(g0 + threadIdx.x + VX_WG * i, total - 1u);
+        const uint32_t b = NB == 1 ? 0u : f / per_col;
+        const uint32_t rem = f - b * per_col;
+        const uint32_t ul = rem >> 4, j = rem & 15u;
+        const int64_t k = 64 * (int64_t)(ub + ul) + 4 * j;
+        if constexpr (XV) {
+            xg.v[i] = *(const f32x4*)(a.x + b * a.xs_b + k);
+        } else {
+            const float* xp = a.x + b * a.xs_b + k * a.xs_k;
+            xg.v[i] = f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+        }
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void vx_stage_store(const vx_gemv_args& a, uint32_t cu, uint32_t g0, const vx_xgroup& xg) {
+    const uint32_t per_col = cu * 16u;
+    const uint32_t total = per_col * NB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t f = g0 + threadIdx.x + VX_WG * i;
+        if (f < total) {
+            const uint32_t b = NB == 1 ? 0u : f / per_col;
+            const uint32_t rem = f - b * per_col;
+            vx_lds_x[(b * 16u + (rem & 15u)) * a.upitch + (rem >> 4)] = xg.v[i];
+        }
+    }
+}
+
+// Groups after the first (only when a chunk holds more than 1024 float4).
+template <int NB, bool XV>
+__device__ __forceinline__ void vx_stage_rest(const vx_gemv_args& a, uint32_t ub, uint32_t cu) {
+    for (uint32_t g0 = 4 * VX_WG; g0 < cu * 16u * NB; g0 += 4 * VX_WG) {
+        vx_xgroup xg;
+        vx_stage_load<NB, XV>(a, ub, cu, g0, xg);
+        vx_stage_store<NB>(a, cu, g0, xg);
+    }
+}
+
+template <int QT, int R, bool XV>
+__device__ __forceinline__ void vx_gemv_b1(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t row0 = (blockIdx.x * 4u + wave) * R;
+
+    const uint8_t* wrow[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rok[r] = row0 + r < a.M;
+        wrow[r] = a.w + (uint64_t)(rok[r] ? row0 + r : 0u) * a.row_stride;
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+    for (uint32_t ub = 0; ub < a.nunits; ub += a.chunk_units) {
+        const uint32_t cu = min(a.chunk_units, a.nunits - ub);
+        // x loads first, then the first pass's weight loads: the LDS stores
+        // of x wait only for x, and the weights' HBM latency overlaps the
+        // staging round trip and the barrier.
+        vx_xgroup xg;
+        vx_stage_load<1, XV>(a, ub, cu, 0, xg);
+        // Loads are unconditional (rows past M read row 0, lanes past the
+        // chunk read its first unit) so no branch hides them from the
+        // wait-count bookkeeping; their contributions are discarded below.
+        uint32_t wr[R][NW];
+#pragma unroll
+        for (int r = 0; r < R; ++r) vx_load_unit<QT>(wrow[r], ub + (lane < cu ? lane : 0u), wr[r]);
+        if (ub) __syncthreads();
+        vx_stage_store<1>(a, cu, 0, xg);
+        vx_stage_rest<1, XV>(a, ub, cu);
+        __syncthreads();
+
+        for (uint32_t p = 0; p < cu; p += 64) {
+            const uint32_t ul = p + lane;
+            const bool act = ul < cu;
+            if (p) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) vx_load_unit<QT>(wrow[r], ub + (act ? ul : 0u), wr[r]);
+            }
+            float xv[64];
+            const uint32_t uls = act ? ul : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const f32x4 t = vx_lds_x[j * a.upitch + uls];
+                xv[4 * j + 0] = t.x; xv[4 * j + 1] = t.y; xv[4 * j + 2] = t.z; xv[4 * j + 3] = t.w;
+            }
+            float sx0 = 0.f, sx1 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) { sx0 += xv[i]; sx1 += xv[32 + i]; }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float d = vx_unit_dot_b1<QT>(wr[r], xv, sx0, sx1, ub + (act ? ul : 0u));
+                acc[r] += act ? d : 0.f;
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = vx_wave_sum(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (rok[r]) a.y[(int64_t)(row0 + r) * a.ys_m] = acc[r];
+    }
+}
+
+// ------------------------------------------------------------------------
+// Integer-dot path. During staging every 32-element block of x (per batch
+// column) is split into two int8 levels with one f32 scale:
+//     x ~= c * (254 * x1 + x2),   c = max|x_blk| / (127 * 254),
+//     x1 = rint(x / (254 c)),  x2 = rint((x - 254 c x1) / c)  (both in +-127)
+// so |x - c (254 x1 + x2)| <= c / 2 ~ 1.6e-5 * max|x_blk|. A weight block
+// then reduces in exact int32 with v_dot4_i32_i8:
+//     T = 254 * sum(q * x1) + sum(q * x2)            (q the block's integers)
+// and contributes d * c * T (minus the format's zero-point / min term).
+// LDS per chunk and batch column: x1 / x2 as [level][4 slots of 16 B][unit]
+// (odd unit pitch), then per 32-block: c, sum(x) (f32) and
+// O = sum(254 x1 + x2) (int32), indexed 2 * unit + half.
+struct vx_i8lds {
+    uint32_t upitch, cu;
+    __device__ __forceinline__ int4* x8(uint32_t b) const {
+        return (int4*)vx_lds_x + (size_t)b * 8u * upitch;
+    }
+    __device__ __forceinline__ float* cs(uint32_t NB, uint32_t b) const {
+        return (float*)((int4*)vx_lds_x + (size_t)NB * 8u * upitch) + (size_t)b * 2u * upitch;
+    }
+    __device__ __forceinline__ float* sx(uint32_t NB, uint32_t b) const { return cs(NB, NB) + (size_t)b * 2u * upitch; }
+    __device__ __forceinline__ int* oz(uint32_t NB, uint32_t b) const {
+        return (int*)(cs(NB, 2 * NB)) + (size_t)b * 2u * upitch;
+    }
+};
+
+__device__ __forceinline__ uint32_t vx_pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+// Quantize one staged group of float4 (see vx_stage_load) and store it.
+// The 8 float4 of a 32-block are 8 consecutive lanes.
+template <int NB>
+__device__ __forceinline__ void vx_stage_store_i8(const vx_gemv_args& a, uint32_t cu, uint32_t g0, const vx_xgroup& xg) {
+    const uint32_t per_col = cu * 16u;
+    const uint32_t total = per_col * NB;
+    const vx_i8lds L{a.upitch, cu};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t f = g0 + threadIdx.x + VX_WG * i;
+        const f32x4 v = xg.v[i];
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        const float c = m * (1.0f / (127.0f * 254.0f));
+        const float inv1 = m > 0.f ? 127.0f / m : 0.f;  // 1 / (254 c)
+        const float inv2 = inv1 * 254.0f;               // 1 / c
+        const float s1 = 254.0f * c;
+        const float e[4] = {v.x, v.y, v.z, v.w};
+        int q1[4], q2[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            q1[t] = (int)rintf(e[t] * inv1);
+            const float r = __builtin_fmaf(-(float)q1[t], s1, e[t]);
+            q2[t] = min(127, max(-127, (int)rintf(r * inv2)));
+        }
+        float sx = (v.x + v.y) + (v.z + v.w);
+        int oz = 254 * (q1[0] + q1[1] + q1[2] + q1[3]) + (q2[0] + q2[1] + q2[2] + q2[3]);
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            sx += __shfl_xor(sx, off, 64);
+            oz += __shfl_xor(oz, off, 64);
+        }
+        if (f < total) {
+            const uint32_t b = NB == 1 ? 0u : f / per_col;
+            const uint32_t rem = f - b * per_col;
+            const uint32_t ul = rem >> 4, j = rem & 15u;
+            uint32_t* x8 = (uint32_t*)L.x8(b);
+            // dword j of the unit's 64 bytes: slot j/4, dword j%4
+            x8[((0u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[0], q1[1], q1[2], q1[3]);
+            x8[((1u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
+            if ((j & 7u) == 0) {
+                const uint32_t idx = 2u * ul + (j >> 3);
+                L.cs(NB, b)[idx] = c;
+                L.sx(NB, b)[idx] = sx;
+                L.oz(NB, b)[idx] = oz;
+            }
+        }
+    }
+}
+
+template <int NB, bool XV>
+__device__ __forceinline__ void vx_stage_rest_i8(const vx_gemv_args& a, uint32_t ub, uint32_t cu) {
+    for (uint32_t g0 = 4 * VX_WG; g0 < cu * 16u * NB; g0 += 4 * VX_WG) {
+        vx_xgroup xg;
+        vx_stage_load<NB, XV>(a, ub, cu, g0, xg);
+        vx_stage_store_i8<NB>(a, cu, g0, xg);
+    }
+}
+
+// One unit of one row against the staged int8 x of one batch column.
+// x1 / x2: the unit's 16 dwords of each level (dword t = weights 4t..4t+3).
+template <int QT>
+__device__ __forceinline__ float vx_unit_dot_i8(const uint32_t (&r)[vx_unit<QT>::NW], const uint32_t (&x1)[16],
+                                                const uint32_t (&x2)[16], const float (&cb)[2], const float (&sxb)[2],
+                                                const int (&ozb)[2], uint32_t u) {
+    if constexpr (QT == VX_Q4_0) {
+        uint32_t q[8];
+        q[0] = __builtin_amdgcn_alignbit(r[1], r[0], 16);
+        q[1] = __builtin_amdgcn_alignbit(r[2], r[1], 16);
+        q[2] = __builtin_amdgcn_alignbit(r[3], r[2], 16);
+        q[3] = __builtin_amdgcn_alignbit(r[4], r[3], 16);
+        q[4] = r[5]; q[5] = r[6]; q[6] = r[7]; q[7] = r[8];
+        float res = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int i1 = 0, i2 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = vx_and(q[4 * h + i], 0x0F0F0F0Fu);
+                const uint32_t hi = vx_and(q[4 * h + i] >> 4, 0x0F0F0F0Fu);
+                i1 = __builtin_amdgcn_sdot4((int)lo, (int)x1[8 * h + i], i1, false);
+                i1 = __builtin_amdgcn_sdot4((int)hi, (int)x1[8 * h + 4 + i], i1, false);
+                i2 = __builtin_amdgcn_sdot4((int)lo, (int)x2[8 * h + i], i2, false);
+                i2 = __builtin_amdgcn_sdot4((int)hi, (int)x2[8 * h + 4 + i], i2, false);
+            }
+            const int t = 254 * i1 + i2 - 8 * ozb[h];
+            const float d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
+            res = __builtin_fmaf(d * cb[h], (float)t, res);
+        }
+        return res;
+    } else if constexpr (QT == VX_Q8_0) {
+        float res = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int i1 = 0, i2 = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t qd = h ? r[9 + i] : __builtin_amdgcn_alignbit(r[i + 1], r[i], 16);
+                i1 = __builtin_amdgcn_sdot4((int)qd, (int)x1[8 * h + i], i1, false);
+                i2 = __builtin_amdgcn_sdot4((int)qd, (int)x2[8 * h + i], i2, false);
+            }
+            const int t = 254 * i1 + i2;
+            const float d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
+            res = __builtin_fmaf(d * cb[h], (float)t, res);
+        }
+        return res;
+    } else {
+        const float d = vx_f16_to_f32(r[0]);
+        const float dmin = vx_f16_to_f32(r[0] >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        vx_q4k_scales(r[1], r[2], r[3], u & 3u, sc0, m0, sc1, m1);
+        int a1 = 0, a2 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = vx_and(r[4 + i], 0x0F0F0F0Fu);
+            const uint32_t hi = vx_and(r[4 + i] >> 4, 0x0F0F0F0Fu);
+            a1 = __builtin_amdgcn_sdot4((int)lo, (int)x1[i], a1, false);
+            a2 = __builtin_amdgcn_sdot4((int)lo, (int)x2[i], a2, false);
+            b1 = __builtin_amdgcn_sdot4((int)hi, (int)x1[8 + i], b1, false);
+            b2 = __builtin_amdgcn_sdot4((int)hi, (int)x2[8 + i], b2, false);
+        }
+        const float t0 = (float)(254 * a1 + a2), t1 = (float)(254 * b1 + b2);
+        float res = __builtin_fmaf(d * (float)sc0 * cb[0], t0, -(dmin * (float)m0) * sxb[0]);
+        res = __builtin_fmaf(d * (float)sc1 * cb[1], t1, res);
+        return __builtin_fmaf(-(dmin * (float)m1), sxb[1], res);
+    }
+}
+
+__device__ __forceinline__ void vx_read_x8(const vx_i8lds& L, uint32_t b, uint32_t ul, uint32_t (&x1)[16],
+                                           uint32_t (&x2)[16]) {
+    const int4* x8 = L.x8(b);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int4 v1 = x8[(0 * 4 + s) * L.upitch + ul];
+        const int4 v2 = x8[(1 * 4 + s) * L.upitch + ul];
+        x1[4 * s + 0] = v1.x; x1[4 * s + 1] = v1.y; x1[4 * s + 2] = v1.z; x1[4 * s + 3] = v1.w;
+        x2[4 * s + 0] = v2.x; x2[4 * s + 1] = v2.y; x2[4 * s + 2] = v2.z; x2[4 * s + 3] = v2.w;
+    }
+}
+
+// Batch 1 on the integer-dot path: same work split as vx_gemv_b1.
+template <int QT, int R, bool XV>
+__device__ __forceinline__ void vx_gemv_i8b1(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t row0 = (blockIdx.x * 4u + wave) * R;
+    const uint8_t* wrow[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rok[r] = row0 + r < a.M;
+        wrow[r] = a.w + (uint64_t)(rok[r] ? row0 + r : 0u) * a.row_stride;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+
+    for (uint32_t ub = 0; ub < a.nunits; ub += a.chunk_units) {
+        const uint32_t cu = min(a.chunk_units, a.nunits - ub);
+        const vx_i8lds L{a.upitch, cu};
+        vx_xgroup xg;
+        vx_stage_load<1, XV>(a, ub, cu, 0, xg);
+        uint32_t wr[R][NW];
+#pragma unroll
+        for (int r = 0; r < R; ++r) vx_load_unit<QT>(wrow[r], ub + (lane < cu ? lane : 0u), wr[r]);
+        if (ub) __syncthreads();
+        vx_stage_store_i8<1>(a, cu, 0, xg);
+        vx_stage_rest_i8<1, XV>(a, ub, cu);
+        __syncthreads();
+
+        for (uint32_t p = 0; p < cu; p += 64) {
+            const uint32_t ul = p + lane;
+            const bool act = ul < cu;
+            const uint32_t uls = act ? ul : 0u;
+            if (p) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) vx_load_unit<QT>(wrow[r], ub + uls, wr[r]);
+            }
+            uint32_t x1[16], x2[16];
+            vx_read_x8(L, 0, uls, x1, x2);
+            const float2 cb2 = *(const float2*)&L.cs(1, 0)[2 * uls];
+            const float2 sx2 = *(const float2*)&L.sx(1, 0)[2 * uls];
+            const int2 oz2 = *(const int2*)&L.oz(1, 0)[2 * uls];
+            const float cb[2] = {cb2.x, cb2.y}, sxb[2] = {sx2.x, sx2.y};
+            const int ozb[2] = {oz2.x, oz2.y};
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float d = vx_unit_dot_i8<QT>(wr[r], x1, x2, cb, sxb, ozb, ub + uls);
+                acc[r] += act ? d : 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = vx_wave_sum(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (rok[r]) a.y[(int64_t)(row0 + r) * a.ys_m] = acc[r];
+    }
+}
+
+// Batch NB > 1: lane l serves row group g = l / LPR (R rows each) and unit
+// l % LPR of each pass; weights are decoded exactly 8 at a time and
+// multiplied with the matching x slots of every batch column from LDS.
+template <int QT, int NB, int R, int LPR, bool XV>
+__device__ __forceinline__ void vx_gemv_bn(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    constexpr int G = 64 / LPR;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t g = lane / LPR, li = lane % LPR;
+    const uint32_t row0 = ((blockIdx.x * 4u + wave) * G + g) * R;
+
+    const uint8_t* wrow[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rok[r] = row0 + r < a.M;
+        wrow[r] = a.w + (uint64_t)(rok[r] ? row0 + r : 0u) * a.row_stride;
+    }
+    float acc[R][NB];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
+
+    for (uint32_t ub = 0; ub < a.nunits; ub += a.chunk_units) {
+        const uint32_t cu = min(a.chunk_units, a.nunits - ub);
+        vx_xgroup xg;
+        vx_stage_load<NB, XV>(a, ub, cu, 0, xg);
+        if (ub) __syncthreads();
+        vx_stage_store<NB>(a, cu, 0, xg);
+        vx_stage_rest<NB, XV>(a, ub, cu);
+        __syncthreads();
+        for (uint32_t p = 0; p < cu; p += LPR) {
+            const uint32_t ul = p + li;
+            const bool act = ul < cu;
+            const uint32_t uls = act ? ul : 0u;
+            uint32_t wr[R][NW];
+#pragma unroll
+            for (int r = 0; r < R; ++r) vx_load_unit<QT>(wrow[r], ub + uls, wr[r]);
+            float sc[R][4];
+#pragma unroll
+            for (int r = 0; r < R; ++r) vx_unit_scales<QT>(wr[r], ub + ul, sc[r]);
+#pragma unroll
+            for (int grp = 0; grp < 8; ++grp) {
+                float wv[R][8];
+                int ja = 0, jb = 0;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    vx_unit_group<QT>(wr[r], sc[r], grp, wv[r], ja, jb);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) wv[r][e] = act ? wv[r][e] : 0.f;
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const f32x4 xa = vx_lds_x[(b * 16 + ja) * a.upitch + uls];
+                    const f32x4 xb = vx_lds_x[(b * 16 + jb) * a.upitch + uls];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float s = acc[r][b];
+                        s = __builtin_fmaf(wv[r][0], xa.x, s);
+                        s = __builtin_fmaf(wv[r][1], xa.y, s);
+                        s = __builtin_fmaf(wv[r][2], xa.z, s);
+                        s = __builtin_fmaf(wv[r][3], xa.w, s);
+                        s = __builtin_fmaf(wv[r][4], xb.x, s);
+                        s = __builtin_fmaf(wv[r][5], xb.y, s);
+                        s = __builtin_fmaf(wv[r][6], xb.z, s);
+                        s = __builtin_fmaf(wv[r][7], xb.w, s);
+                        acc[r][b] = s;
+                    }
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[r][b] = vx_group_sum(acc[r][b], LPR);
+    if (li == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (rok[r]) {
+#pragma unroll
+                for (int b = 0; b < NB; ++b) a.y[(int64_t)(row0 + r) * a.ys_m + (int64_t)b * a.ys_b] = acc[r][b];
+            }
+    }
+}
+
+// Any layout fallback (K a multiple of 32, any alignment, any B): one
+// wave per row, lane l decodes 32-weight groups l, l+64, ... byte by byte.
+template <int QT>
+__device__ __forceinline__ void vx_gemv_generic(const vx_gemv_args& a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (row >= a.M) return;  // wave-uniform; no barrier in this kernel
+    const uint8_t* wrow = a.w + (uint64_t)row * a.row_stride;
+    const uint32_t ngroups = a.K / 32u;
+    for (uint32_t b = 0; b < a.B; ++b) {
+        float acc = 0.f;
+        for (uint32_t kb = lane; kb < ngroups; kb += 64) {
+            float o[32];
+            vx_decode32<QT>(wrow, kb, o);
+            const float* xp = a.x + (int64_t)b * a.xs_b + (int64_t)(32 * kb) * a.xs_k;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) acc = __builtin_fmaf(o[i], xp[(int64_t)i * a.xs_k], acc);
+        }
+        acc = vx_wave_sum(acc);
+        if (lane == 0) a.y[(int64_t)row * a.ys_m + (int64_t)b * a.ys_b] = acc;
+    }
+}
+
+// out[m, k] = decode(W)[m, k]; thread per 32-weight group. Output view:
+// element (m, k) at y[m * ys_m + k * ys_b].
+template <int QT>
+__device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
+    const uint32_t ngroups = a.K / 32u;
+    const uint64_t t = (uint64_t)blockIdx.x * VX_WG + threadIdx.x;
+    if (t >= (uint64_t)a.M * ngroups) return;
+    const uint32_t m = (uint32_t)(t / ngroups), kb = (uint32_t)(t % ngroups);
+    float o[32];
+    vx_decode32<QT>(a.w + (uint64_t)m * a.row_stride, kb, o);
+    float* op = a.y + (int64_t)m * a.ys_m + (int64_t)(32 * kb) * a.ys_b;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) op[(int64_t)i * a.ys_b] = o[i];
+}
+
+#define VX_GEMV_B1(QT, QN, R)                                                              \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_b1_##QN##_r##R(vx_gemv_args a) { \
+        if (a.x_vec) vx_gemv_b1<QT, R, true>(a);                                           \
+        else vx_gemv_b1<QT, R, false>(a);                                                  \
+    }
+#define VX_GEMV_I8B1(QT, QN, R)                                                               \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_i8b1_##QN##_r##R(vx_gemv_args a) { \
+        if (a.x_vec) vx_gemv_i8b1<QT, R, true>(a);                                           \
+        else vx_gemv_i8b1<QT, R, false>(a);                                                  \
+    }
+#define VX_GEMV_BN(QT, QN, NB, R, LPR)                                                            \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_b##NB##_##QN##_r##R(vx_gemv_args a) { \
+        if (a.x_vec) vx_gemv_bn<QT, NB, R, LPR, true>(a);                                         \
+        else vx_gemv_bn<QT, NB, R, LPR, false>(a);                                                \
+    }
+#define VX_GEMV_ALL(QT, QN)                                                                         \
+    VX_GEMV_B1(QT, QN, 1)                                                                           \
+    VX_GEMV_B1(QT, QN, 2)                                                                           \
+    VX_GEMV_B1(QT, QN, 4)                                                                           \
+    VX_GEMV_B1(QT, QN, 8)                                                                           \
+    VX_GEMV_I8B1(QT, QN, 1)                                                                         \
+    VX_GEMV_I8B1(QT, QN, 2)                                                                         \
+    VX_GEMV_I8B1(QT, QN, 4)                                                                         \
+    VX_GEMV_I8B1(QT, QN, 8)                                                                         \
+    VX_GEMV_BN(QT, QN, 2, 2, 64)                                                                    \
+    VX_GEMV_BN(QT, QN, 4, 2, 64)                                                                    \
+    VX_GEMV_BN(QT, QN, 8, 2, 32)                                                                    \
+    VX_GEMV_BN(QT, QN, 16, 2, 16)                                                                   \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_generic_##QN(vx_gemv_args a) {     \
+        vx_gemv_generic<QT>(a);                                                                     \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_dequant_##QN(vx_gemv_args a) { vx_dequant<QT>(a); }
+
+VX_GEMV_ALL(VX_Q4_0, q4_0)
+VX_GEMV_ALL(VX_Q8_0, q8_0)
+VX_GEMV_ALL(VX_Q4_K, q4_k)

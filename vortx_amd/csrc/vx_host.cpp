@@ -1,0 +1,645 @@
+// vx_host.cpp — runtime and op dispatch of libvortx_hip.so behind the C ABI
+// declared in include/vortx_hip.h.
+//
+// Runtime: the gfx950 code objects built by hipcc --genco are embedded in
+// this library (vx_embed.S); vx_init loads them with hipModuleLoadData and
+// resolves every kernel once; launches go through hipModuleLaunchKernel with
+// the kernel's argument struct (vx_kargs.h) passed by value.
+//
+// Ops: Gemm::dispatch / dispatch_naive / dispatch_tiled of
+// src/linalg/gemm.rs:47-305 (canonicalize, validate, pick a kernel, grid)
+// and the block-quantized GEMV / dequantize, which the reference lacks.
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "vx_internal.hpp"
+#include "vx_kargs.h"
+
+extern "C" {
+extern const unsigned char vx_co_gemm[];
+extern const unsigned char vx_co_gemm_end[];
+extern const unsigned char vx_co_gemv_q[];
+extern const unsigned char vx_co_gemv_q_end[];
+}
+
+namespace vx {
+
+// --------------------------------------------------------------- errors
+static thread_local std::string t_msg;
+static thread_local int t_hip = 0;
+
+int fail(int status, const char* msg) {
+    t_msg = msg ? msg : "";
+    return status;
+}
+
+int fail_hip(int hip_error, const char* what) {
+    t_hip = hip_error;
+    t_msg = std::string(what) + ": " + hipGetErrorString((hipError_t)hip_error);
+    return VX_ERR_HIP;
+}
+
+static void clear_error() {
+    t_msg.clear();
+    t_hip = 0;
+}
+
+// -------------------------------------------------------------- kernels
+// Every kernel the library launches; resolved by name at vx_init.
+enum Kernel : int {
+#define K(name) K_##name,
+#include "vx_kernel_list.inc"
+#undef K
+    K_COUNT
+};
+static const char* const kKernelNames[K_COUNT] = {
+#define K(name) #name,
+#include "vx_kernel_list.inc"
+#undef K
+};
+static bool kernel_in_gemm_module(int k) { return k <= K_vx_gemv_f32; }
+
+}  // namespace vx
+
+struct vx_context {
+    int device = 0;
+    int num_cus = 0;
+    size_t lds_per_block = 65536;
+    hipModule_t mod_gemm = nullptr;
+    hipModule_t mod_gemv = nullptr;
+    hipFunction_t fn[vx::K_COUNT] = {};
+};
+
+namespace vx {
+
+struct DeviceGuard {
+    int prev = -1;
+    bool changed = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+            changed = hipSetDevice(dev) == hipSuccess;
+        }
+    }
+    ~DeviceGuard() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+template <class Args>
+static int launch(vx_ctx ctx, int k, dim3 grid, dim3 block, size_t lds, vx_stream stream, const Args& args) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return VX_OK;
+    Args copy = args;
+    size_t size = sizeof(Args);
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &copy, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                      HIP_LAUNCH_PARAM_END};
+    const hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                               (unsigned)lds, (hipStream_t)stream, nullptr, config);
+    if (e != hipSuccess) return fail_hip(e, kKernelNames[k]);
+    return VX_OK;
+}
+
+// ----------------------------------------------------------------- init
+static int init(int device, vx_ctx* out) {
+    if (!out) return fail(VX_ERR_INVALID, "null out_ctx");
+    *out = nullptr;
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess) return fail_hip(e, "hipGetDeviceCount");
+    if (device < 0 || device >= ndev) return fail(VX_ERR_INVALID, "device ordinal out of range");
+    DeviceGuard guard(device);
+    if (!guard.changed) {
+        int cur = -1;
+        if (hipGetDevice(&cur) != hipSuccess || cur != device) {
+            e = hipSetDevice(device);
+            if (e != hipSuccess) return fail_hip(e, "hipSetDevice");
+        }
+    }
+    auto* ctx = new vx_context();
+    ctx->device = device;
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail_hip(e, "hipGetDeviceProperties");
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        delete ctx;
+        return fail(VX_ERR_UNSUPPORTED, "device is not gfx950 (MI355X); this library ships gfx950 code only");
+    }
+    ctx->num_cus = prop.multiProcessorCount;
+    ctx->lds_per_block = prop.sharedMemPerBlock;
+    e = hipModuleLoadData(&ctx->mod_gemm, vx_co_gemm);
+    if (e == hipSuccess) e = hipModuleLoadData(&ctx->mod_gemv, vx_co_gemv_q);
+    if (e != hipSuccess) {
+        if (ctx->mod_gemm) (void)hipModuleUnload(ctx->mod_gemm);
+        t_hip = e;
+        t_msg = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
+        delete ctx;
+        return VX_ERR_NO_CODE_OBJECT;
+    }
+    for (int k = 0; k < K_COUNT; ++k) {
+        hipModule_t m = kernel_in_gemm_module(k) ? ctx->mod_gemm : ctx->mod_gemv;
+        e = hipModuleGetFunction(&ctx->fn[k], m, kKernelNames[k]);
+        if (e != hipSuccess) {
+            (void)hipModuleUnload(ctx->mod_gemm);
+            (void)hipModuleUnload(ctx->mod_gemv);
+            delete ctx;
+            t_hip = e;
+            t_msg = std::string("hipModuleGetFunction(") + kKernelNames[k] + "): " + hipGetErrorString(e);
+            return VX_ERR_NO_CODE_OBJECT;
+        }
+    }
+    *out = ctx;
+    return VX_OK;
+}
+
+// ------------------------------------------------------------ view math
+struct Canon {
+    vx_layout l;      // canonical rank-4 layout (offset applied to ptr)
+    uintptr_t ptr;    // base + original offset, in bytes
+};
+
+static int canon_view(const void* base, const vx_layout* in, Canon* c, const char* name) {
+    if (!in) return fail(VX_ERR_INVALID, "null view");
+    if (in->rank > 4) return fail(VX_ERR_UNSUPPORTED, "tensors of ranks > 4 not supported");
+    int s = layout_canonicalize(in, &c->l);
+    if (s) return s;
+    c->ptr = (uintptr_t)base + 4ull * in->offset;
+    uint64_t n = 1;
+    for (int k = 0; k < 4; ++k) n *= c->l.size[k];
+    if (n && !base) {
+        static thread_local std::string m;
+        m = std::string("null base pointer for ") + name;
+        return fail(VX_ERR_INVALID, m.c_str());
+    }
+    return VX_OK;
+}
+
+static bool aligned16(uintptr_t p) { return (p & 15u) == 0; }
+
+static std::string layout_str(const vx_layout& l) {
+    char buf[200];
+    std::snprintf(buf, sizeof buf, "{size:[%u,%u,%u,%u], stride:[%u,%u,%u,%u]}", l.size[0], l.size[1], l.size[2],
+                  l.size[3], l.stride[0], l.stride[1], l.stride[2], l.stride[3]);
+    return buf;
+}
+
+// ---------------------------------------------------------------- gemm
+enum Force { FORCE_AUTO = -1, FORCE_NAIVE = 0, FORCE_TILED = 1 };
+
+struct GemmPlan {
+    Canon o, l, r;
+    uint32_t M, N, K, nb, nc;
+    int route;
+};
+
+// Canonicalize and validate exactly like Gemm::dispatch
+// (src/linalg/gemm.rs:66-104), then choose the route (:111-118).
+static int plan_gemm(const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs, int force, GemmPlan* p) {
+    if (!out || !lhs || !rhs) return fail(VX_ERR_INVALID, "null view");
+    int s;
+    if ((s = canon_view(out->base, &out->layout, &p->o, "out"))) return s;
+    if ((s = canon_view(lhs->base, &lhs->layout, &p->l, "lhs"))) return s;
+    if ((s = canon_view(rhs->base, &rhs->layout, &p->r, "rhs"))) return s;
+    const vx_layout &so = p->o.l, &sl = p->l.l, &sr = p->r.l;
+    const bool ok = so.size[0] == sl.size[0] && so.size[1] == sl.size[1] && sl.size[0] == sr.size[0] &&
+                    sl.size[1] == sr.size[1] && so.size[2] == sl.size[2] && so.size[3] == sr.size[3] &&
+                    sl.size[3] == sr.size[2];
+    if (!ok) {
+        static thread_local std::string m;
+        m = "incompatible gemm shapes: " + layout_str(so) + " = " + layout_str(sl) + " x " + layout_str(sr);
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    p->nb = so.size[0];
+    p->nc = so.size[1];
+    p->M = so.size[2];
+    p->N = so.size[3];
+    p->K = sl.size[3];
+    if ((uint64_t)p->nb * p->nc > 65535u) return fail(VX_ERR_UNSUPPORTED, "more than 65535 batch matrices");
+    if (p->M == 0 || p->N == 0 || p->nb == 0 || p->nc == 0) {
+        p->route = VX_ROUTE_EMPTY;
+        return VX_OK;
+    }
+    if (force == FORCE_NAIVE) {
+        p->route = VX_ROUTE_NAIVE;
+    } else if (force == FORCE_TILED) {
+        p->route = VX_ROUTE_TILED;
+    } else if (p->M < 32 && p->N < 32) {
+        p->route = VX_ROUTE_NAIVE;
+    } else if (p->N == 1 && sl.stride[3] == 1 && sl.stride[2] % 4 == 0 && (p->nb == 1 || sl.stride[0] % 4 == 0) &&
+               (p->nc == 1 || sl.stride[1] % 4 == 0) && aligned16(p->l.ptr)) {
+        p->route = VX_ROUTE_GEMV;
+    } else {
+        p->route = VX_ROUTE_TILED;
+    }
+    return VX_OK;
+}
+
+// Operand mode for the MFMA kernel: 0 = contiguous along K, 1 = contiguous
+// along the other dim (M for A, N for B), 2 = generic. 128-bit loads need
+// the unit-stride dim plus 4-aligned other strides and a 16-byte base.
+static int operand_mode(const Canon& c, int kdim, int xdim, uint32_t nb, uint32_t nc) {
+    const vx_layout& l = c.l;
+    const bool batch4 = (nb == 1 || l.stride[0] % 4 == 0) && (nc == 1 || l.stride[1] % 4 == 0);
+    if (!batch4 || !aligned16(c.ptr)) return 2;
+    if (l.stride[kdim] == 1 && l.stride[xdim] % 4 == 0) return 0;
+    if (l.stride[xdim] == 1 && l.stride[kdim] % 4 == 0) return 1;
+    return 2;
+}
+
+static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs,
+                    int force) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    GemmPlan p;
+    int s = plan_gemm(out, lhs, rhs, force, &p);
+    if (s) return s;
+    if (p.route == VX_ROUTE_EMPTY) return VX_OK;
+    DeviceGuard guard(ctx->device);
+    const uint32_t batch = p.nb * p.nc;
+    if (p.route == VX_ROUTE_GEMV) {
+        vx_gemv_f32_args g{};
+        g.a = (const float*)p.l.ptr;
+        g.as_m = p.l.l.stride[2];
+        g.as_k = p.l.l.stride[3];
+        g.x = (const float*)p.r.ptr;
+        g.xs_k = p.r.l.stride[2];
+        g.y = (float*)p.o.ptr;
+        g.ys_m = p.o.l.stride[2];
+        g.M = p.M;
+        g.K = p.K;
+        g.batch_c = p.nc;
+        g.a_bs[0] = p.l.l.stride[0];
+        g.a_bs[1] = p.l.l.stride[1];
+        g.x_bs[0] = p.r.l.stride[0];
+        g.x_bs[1] = p.r.l.stride[1];
+        g.y_bs[0] = p.o.l.stride[0];
+        g.y_bs[1] = p.o.l.stride[1];
+        return launch(ctx, K_vx_gemv_f32, dim3((p.M + 3) / 4, batch, 1), dim3(VX_WG), 0, stream, g);
+    }
+    vx_gemm_args a{};
+    a.c = (float*)p.o.ptr;
+    a.a = (const float*)p.l.ptr;
+    a.b = (const float*)p.r.ptr;
+    for (int k = 0; k < 4; ++k) {
+        a.cs[k] = p.o.l.stride[k];
+        a.as[k] = p.l.l.stride[k];
+        a.bs[k] = p.r.l.stride[k];
+    }
+    a.batch_c = p.nc;
+    a.M = p.M;
+    a.N = p.N;
+    a.K = p.K;
+    if (p.route == VX_ROUTE_NAIVE) {
+        return launch(ctx, K_vx_gemm_naive, dim3((p.N + 63) / 64, p.M, batch), dim3(64), 0, stream, a);
+    }
+    a.tiles_m = (p.M + 127) / 128;
+    a.tiles_n = (p.N + 127) / 128;
+    const int am = operand_mode(p.l, 3, 2, p.nb, p.nc);
+    const int bm = operand_mode(p.r, 2, 3, p.nb, p.nc);
+    int k;
+    if (am == 0 && bm == 1) k = K_vx_gemm_mfma_kx;
+    else if (am == 0 && bm == 0) k = K_vx_gemm_mfma_kk;
+    else if (am == 1 && bm == 1) k = K_vx_gemm_mfma_xx;
+    else if (am == 1 && bm == 0) k = K_vx_gemm_mfma_xk;
+    else if (am == 0) k = K_vx_gemm_mfma_kg;
+    else if (bm == 1) k = K_vx_gemm_mfma_gx;
+    else k = K_vx_gemm_mfma_gg;
+    const uint64_t tiles = (uint64_t)a.tiles_m * a.tiles_n;
+    if (tiles > 0x7FFFFFFFull) return fail(VX_ERR_UNSUPPORTED, "too many output tiles");
+    return launch(ctx, k, dim3((uint32_t)tiles, 1, batch), dim3(VX_WG), 0, stream, a);
+}
+
+// ------------------------------------------------------------ quant gemv
+static int qinfo(uint32_t qt, uint32_t* qk, uint32_t* bb) {
+    switch (qt) {
+    case VX_Q4_0: *qk = 32; *bb = 18; return VX_OK;
+    case VX_Q8_0: *qk = 32; *bb = 34; return VX_OK;
+    case VX_Q4_K: *qk = 256; *bb = 144; return VX_OK;
+    default: return fail(VX_ERR_INVALID, "unknown quant type (expected GGML id 2, 8 or 12)");
+    }
+}
+
+static int check_qweight(const vx_qweight* w, uint32_t* qk, uint32_t* bb) {
+    if (!w) return fail(VX_ERR_INVALID, "null weight");
+    int s = qinfo(w->qtype, qk, bb);
+    if (s) return s;
+    if (w->reserved) return fail(VX_ERR_INVALID, "vx_qweight.reserved must be 0");
+    if (w->cols % *qk) return fail(VX_ERR_UNSUPPORTED, "cols is not a multiple of the block size");
+    if (w->row_stride_bytes < (uint64_t)(w->cols / *qk) * *bb)
+        return fail(VX_ERR_INVALID, "row_stride_bytes smaller than one row of blocks");
+    if (w->rows && w->cols && !w->base) return fail(VX_ERR_INVALID, "null weight base");
+    return VX_OK;
+}
+
+static int q_index(uint32_t qt) { return qt == VX_Q4_0 ? 0 : qt == VX_Q8_0 ? 1 : 2; }
+
+static int b1_kernel(uint32_t qt, int R) {
+    static const int tab[3][4] = {
+        {K_vx_gemv_b1_q4_0_r1, K_vx_gemv_b1_q4_0_r2, K_vx_gemv_b1_q4_0_r4, K_vx_gemv_b1_q4_0_r8},
+        {K_vx_gemv_b1_q8_0_r1, K_vx_gemv_b1_q8_0_r2, K_vx_gemv_b1_q8_0_r4, K_vx_gemv_b1_q8_0_r8},
+        {K_vx_gemv_b1_q4_k_r1, K_vx_gemv_b1_q4_k_r2, K_vx_gemv_b1_q4_k_r4, K_vx_gemv_b1_q4_k_r8}};
+    const int ri = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;
+    return tab[q_index(qt)][ri];
+}
+
+static int i8b1_kernel(uint32_t qt, int R) {
+    static const int tab[3][4] = {
+        {K_vx_gemv_i8b1_q4_0_r1, K_vx_gemv_i8b1_q4_0_r2, K_vx_gemv_i8b1_q4_0_r4, K_vx_gemv_i8b1_q4_0_r8},
+        {K_vx_gemv_i8b1_q8_0_r1, K_vx_gemv_i8b1_q8_0_r2, K_vx_gemv_i8b1_q8_0_r4, K_vx_gemv_i8b1_q8_0_r8},
+        {K_vx_gemv_i8b1_q4_k_r1, K_vx_gemv_i8b1_q4_k_r2, K_vx_gemv_i8b1_q4_k_r4, K_vx_gemv_i8b1_q4_k_r8}};
+    const int ri = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;
+    return tab[q_index(qt)][ri];
+}
+
+static int bn_kernel(uint32_t qt, int NB) {
+    static const int tab[3][4] = {
+        {K_vx_gemv_b2_q4_0_r2, K_vx_gemv_b4_q4_0_r2, K_vx_gemv_b8_q4_0_r2, K_vx_gemv_b16_q4_0_r2},
+        {K_vx_gemv_b2_q8_0_r2, K_vx_gemv_b4_q8_0_r2, K_vx_gemv_b8_q8_0_r2, K_vx_gemv_b16_q8_0_r2},
+        {K_vx_gemv_b2_q4_k_r2, K_vx_gemv_b4_q4_k_r2, K_vx_gemv_b8_q4_k_r2, K_vx_gemv_b16_q4_k_r2}};
+    const int ni = NB == 2 ? 0 : NB == 4 ? 1 : NB == 8 ? 2 : 3;
+    return tab[q_index(qt)][ni];
+}
+
+static int generic_kernel(uint32_t qt) {
+    return qt == VX_Q4_0 ? K_vx_gemv_generic_q4_0 : qt == VX_Q8_0 ? K_vx_gemv_generic_q8_0 : K_vx_gemv_generic_q4_k;
+}
+
+static int dequant_kernel(uint32_t qt) {
+    return qt == VX_Q4_0 ? K_vx_dequant_q4_0 : qt == VX_Q8_0 ? K_vx_dequant_q8_0 : K_vx_dequant_q4_k;
+}
+
+// Rows per wave for batch 1: the largest R whose grid still gives every
+// CU at least two workgroups (VX_GEMV_R overrides, for tuning sweeps).
+static int pick_rows_per_wave(vx_ctx ctx, uint32_t qt, uint32_t M) {
+    if (const char* e = std::getenv("VX_GEMV_R")) {
+        const int r = std::atoi(e);
+        if (r == 1 || r == 2 || r == 4 || r == 8) return r;
+    }
+    const int maxr = qt == VX_Q8_0 ? 4 : 8;
+    for (int r = maxr; r > 1; r >>= 1)
+        if ((M + 4u * r - 1) / (4u * r) >= 2u * (uint32_t)ctx->num_cus) return r;
+    return 1;
+}
+
+static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
+                      uint32_t flags) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    uint32_t qk, bb;
+    int s = check_qweight(w, &qk, &bb);
+    if (s) return s;
+    if (!y || !x) return fail(VX_ERR_INVALID, "null view");
+    if (y->layout.rank < 1 || y->layout.rank > 2 || x->layout.rank < 1 || x->layout.rank > 2)
+        return fail(VX_ERR_SHAPE, "y must be [M] or [M, B] and x [K] or [K, B]");
+    // A rank-1 y / x is a column ([M] -> [M, 1], [K] -> [K, 1]).
+    vx_layout ly = y->layout, lx = x->layout;
+    if (ly.rank == 1 && (s = layout_unsqueeze(&y->layout, 1, &ly))) return s;
+    if (lx.rank == 1 && (s = layout_unsqueeze(&x->layout, 1, &lx))) return s;
+    Canon cy, cx;
+    if ((s = canon_view(y->base, &ly, &cy, "y"))) return s;
+    if ((s = canon_view(x->base, &lx, &cx, "x"))) return s;
+    const uint32_t M = w->rows, K = w->cols;
+    const uint32_t B = cy.l.size[3];
+    if (cy.l.size[2] != M || cx.l.size[2] != K || cx.l.size[3] != B) {
+        static thread_local std::string m;
+        m = "incompatible gemv shapes: y " + layout_str(cy.l) + " = W [" + std::to_string(M) + ", " +
+            std::to_string(K) + "] x " + layout_str(cx.l);
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    if (M == 0 || B == 0) return VX_OK;
+    DeviceGuard guard(ctx->device);
+
+    vx_gemv_args a{};
+    a.w = (const uint8_t*)w->base;
+    a.row_stride = w->row_stride_bytes;
+    a.xs_k = cx.l.stride[2];
+    a.xs_b = cx.l.stride[3];
+    a.ys_m = cy.l.stride[2];
+    a.ys_b = cy.l.stride[3];
+    a.M = M;
+    a.K = K;
+    a.nunits = K / 64;
+
+    const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
+    const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
+    uint32_t b0 = 0;
+    while (b0 < B) {
+        const uint32_t rem = B - b0;
+        const int NB = rem >= 16 ? 16 : rem >= 8 ? 8 : rem >= 4 ? 4 : rem >= 2 ? 2 : 1;
+        a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
+        a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
+        a.B = NB;
+        a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (NB == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
+        if (!fast) {
+            a.B = rem;
+            return launch(ctx, generic_kernel(w->qtype), dim3((M + 3) / 4), dim3(VX_WG), 0, stream, a);
+        }
+        int k;
+        uint32_t rows_per_wg;
+        size_t lds;
+        if (NB == 1 && (flags & VX_GEMV_X_INT8)) {
+            // integer-dot path: 152 bytes of LDS per staged unit
+            const int R = pick_rows_per_wave(ctx, w->qtype, M);
+            uint32_t cu = a.nunits;
+            const uint32_t cap = (uint32_t)(budget < 65536 ? budget : 65536) / 152u - 1u;
+            if (cu > cap) cu = cap;
+            a.chunk_units = cu;
+            a.upitch = cu | 1u;
+            k = i8b1_kernel(w->qtype, R);
+            rows_per_wg = 4u * R;
+            lds = (size_t)a.upitch * 152u;
+        } else if (NB == 1) {
+            const int R = pick_rows_per_wave(ctx, w->qtype, M);
+            // x chunk: up to 255 units (16 slots x odd pitch x 16 B <= 64 KB)
+            uint32_t cu = a.nunits;
+            const uint32_t cap = (uint32_t)(budget < 65536 ? budget : 65536) / 256u - 1u;
+            if (cu > cap) cu = cap;
+            a.chunk_units = cu;
+            a.upitch = cu | 1u;
+            k = b1_kernel(w->qtype, R);
+            rows_per_wg = 4u * R;
+            lds = (size_t)NB * 16u * a.upitch * 16u;
+        } else {
+            const uint32_t LPR = NB <= 4 ? 64u : NB == 8 ? 32u : 16u;
+            // Largest multiple of LPR whose [NB][16][pitch] float4 block fits.
+            // An odd pitch keeps the staging stores conflict free; an even
+            // one is used when the odd pitch would not fit.
+            uint32_t cu = LPR;
+            while (cu + LPR <= ((a.nunits + LPR - 1) / LPR) * LPR &&
+                   (size_t)NB * 16u * (cu + LPR) * 16u <= budget)
+                cu += LPR;
+            if ((size_t)NB * 16u * cu * 16u > budget) return fail(VX_ERR_UNSUPPORTED, "LDS budget too small");
+            a.chunk_units = cu;
+            a.upitch = ((size_t)NB * 16u * (cu | 1u) * 16u <= budget) ? (cu | 1u) : cu;
+            k = bn_kernel(w->qtype, NB);
+            rows_per_wg = 4u * (64u / LPR) * 2u;
+            lds = (size_t)NB * 16u * a.upitch * 16u;
+        }
+        s = launch(ctx, k, dim3((M + rows_per_wg - 1) / rows_per_wg), dim3(VX_WG), lds, stream, a);
+        if (s) return s;
+        b0 += NB;
+    }
+    return VX_OK;
+}
+
+static int run_dequant(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    uint32_t qk, bb;
+    int s = check_qweight(w, &qk, &bb);
+    if (s) return s;
+    if (!out) return fail(VX_ERR_INVALID, "null view");
+    if (out->layout.rank != 2) return fail(VX_ERR_SHAPE, "dequantize output must be a rank-2 [M, K] view");
+    Canon co;
+    if ((s = canon_view(out->base, &out->layout, &co, "out"))) return s;
+    if (co.l.size[2] != w->rows || co.l.size[3] != w->cols) return fail(VX_ERR_SHAPE, "output view is not [M, K]");
+    const uint64_t groups = (uint64_t)w->rows * (w->cols / 32u);
+    if (!groups) return VX_OK;
+    if ((groups + VX_WG - 1) / VX_WG > 0x7FFFFFFFull) return fail(VX_ERR_UNSUPPORTED, "matrix too large");
+    DeviceGuard guard(ctx->device);
+    vx_gemv_args a{};
+    a.w = (const uint8_t*)w->base;
+    a.row_stride = w->row_stride_bytes;
+    a.y = (float*)co.ptr;
+    a.ys_m = co.l.stride[2];
+    a.ys_b = co.l.stride[3];
+    a.M = w->rows;
+    a.K = w->cols;
+    return launch(ctx, dequant_kernel(w->qtype), dim3((uint32_t)((groups + VX_WG - 1) / VX_WG)), dim3(VX_WG), 0,
+                  stream, a);
+}
+
+}  // namespace vx
+
+// ================================================================= C ABI
+extern "C" {
+
+int vx_init(int device, vx_ctx* out_ctx) {
+    vx::clear_error();
+    return vx::init(device, out_ctx);
+}
+
+int vx_destroy(vx_ctx ctx) {
+    vx::clear_error();
+    if (!ctx) return VX_OK;
+    vx::DeviceGuard guard(ctx->device);
+    if (ctx->mod_gemm) (void)hipModuleUnload(ctx->mod_gemm);
+    if (ctx->mod_gemv) (void)hipModuleUnload(ctx->mod_gemv);
+    delete ctx;
+    return VX_OK;
+}
+
+int vx_device_info(vx_ctx ctx, int* device, int* num_cus) {
+    if (!ctx) return vx::fail(VX_ERR_INVALID, "null ctx");
+    if (device) *device = ctx->device;
+    if (num_cus) *num_cus = ctx->num_cus;
+    return VX_OK;
+}
+
+int vx_gemm_f32(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs) {
+    return vx::run_gemm(ctx, stream, out, lhs, rhs, vx::FORCE_AUTO);
+}
+
+int vx_gemm_f32_naive(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs) {
+    return vx::run_gemm(ctx, stream, out, lhs, rhs, vx::FORCE_NAIVE);
+}
+
+int vx_gemm_f32_tiled(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs) {
+    return vx::run_gemm(ctx, stream, out, lhs, rhs, vx::FORCE_TILED);
+}
+
+int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs, int* route) {
+    vx::clear_error();
+    if (!route) return vx::fail(VX_ERR_INVALID, "null route");
+    vx::GemmPlan p;
+    const int s = vx::plan_gemm(out, lhs, rhs, vx::FORCE_AUTO, &p);
+    if (s) return s;
+    *route = p.route;
+    return VX_OK;
+}
+
+int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x) {
+    return vx::run_gemv_q(ctx, stream, y, w, x, 0u);
+}
+
+int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
+                 uint32_t flags) {
+    if (flags & ~(uint32_t)VX_GEMV_X_INT8) return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_ex flags");
+    return vx::run_gemv_q(ctx, stream, y, w, x, flags);
+}
+
+int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
+    return vx::run_dequant(ctx, stream, out, w);
+}
+
+int vx_qtype_info(uint32_t qtype, uint32_t* block_weights, uint32_t* block_bytes) {
+    vx::clear_error();
+    uint32_t qk, bb;
+    const int s = vx::qinfo(qtype, &qk, &bb);
+    if (s) return s;
+    if (block_weights) *block_weights = qk;
+    if (block_bytes) *block_bytes = bb;
+    return VX_OK;
+}
+
+int vx_layout_contiguous(const uint32_t* size, uint32_t rank, vx_layout* out) {
+    vx::clear_error();
+    if (!out) return vx::fail(VX_ERR_INVALID, "null out");
+    return vx::layout_contiguous(size, rank, out);
+}
+int vx_layout_canonicalize(const vx_layout* in, vx_layout* out) {
+    vx::clear_error();
+    if (!in || !out) return vx::fail(VX_ERR_INVALID, "null layout");
+    return vx::layout_canonicalize(in, out);
+}
+int vx_layout_transpose(const vx_layout* in, uint32_t a, uint32_t b, vx_layout* out) {
+    vx::clear_error();
+    if (!in || !out) return vx::fail(VX_ERR_INVALID, "null layout");
+    return vx::layout_transpose(in, a, b, out);
+}
+int vx_layout_broadcast(const vx_layout* a, const vx_layout* b, vx_layout* a_out, vx_layout* b_out) {
+    vx::clear_error();
+    if (!a || !b || !a_out || !b_out) return vx::fail(VX_ERR_INVALID, "null layout");
+    return vx::layout_broadcast(a, b, a_out, b_out);
+}
+int vx_layout_view(const vx_layout* in, uint32_t offset, const uint32_t* shape, uint32_t rank,
+                   const uint32_t* strides, uint32_t nstrides, vx_layout* out) {
+    vx::clear_error();
+    if (!in || !out || (rank && !shape)) return vx::fail(VX_ERR_INVALID, "null argument");
+    return vx::layout_view(in, offset, shape, rank, strides, nstrides, out);
+}
+int vx_layout_narrow(const vx_layout* in, uint32_t axis, uint32_t first, uint32_t count, vx_layout* out) {
+    vx::clear_error();
+    if (!in || !out) return vx::fail(VX_ERR_INVALID, "null layout");
+    return vx::layout_narrow(in, axis, first, count, out);
+}
+int vx_layout_unsqueeze(const vx_layout* in, uint32_t axis, vx_layout* out) {
+    vx::clear_error();
+    if (!in || !out) return vx::fail(VX_ERR_INVALID, "null layout");
+    return vx::layout_unsqueeze(in, axis, out);
+}
+int vx_layout_is_contiguous(const vx_layout* in) { return in && vx::layout_is_contiguous(in) ? 1 : 0; }
+
+const char* vx_status_string(int status) {
+    switch (status) {
+    case VX_OK: return "VX_OK";
+    case VX_ERR_SHAPE: return "VX_ERR_SHAPE";
+    case VX_ERR_UNSUPPORTED: return "VX_ERR_UNSUPPORTED";
+    case VX_ERR_INVALID: return "VX_ERR_INVALID";
+    case VX_ERR_HIP: return "VX_ERR_HIP";
+    case VX_ERR_NO_CODE_OBJECT: return "VX_ERR_NO_CODE_OBJECT";
+    default: return "VX_ERR_UNKNOWN";
+    }
+}
+
+const char* vx_last_error_message(void) { return vx::t_msg.c_str(); }
+int vx_last_hip_error(void) { return vx::t_hip; }
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+/*
+ * vx_kargs.h — kernel argument blocks shared by the host library (g++)
+ * and the gfx950 kernels (hipcc). Each kernel takes one of these structs
+ * by value; the host passes it to hipModuleLaunchKernel through
+ * HIP_LAUNCH_PARAM_BUFFER_POINTER, so the layout must be identical on both
+ * sides: only fixed-width integers and pointers, naturally aligned.
+ */
+#ifndef VX_KARGS_H
+#define VX_KARGS_H
+
+#include <stdint.h>
+
+#define VX_WG 256          /* threads per workgroup (4 wave64) */
+#define VX_LDS_X_BYTES 65536 /* LDS budget for staged activations */
+
+/* Dense f32 GEMM on canonical [n, c, rows, cols] operands. Base pointers
+ * already include each view's element offset. Strides in elements. */
+typedef struct vx_gemm_args {
+    float* c;
+    const float* a;
+    const float* b;
+    int64_t cs[4];
+    int64_t as[4];
+    int64_t bs[4];
+    uint32_t batch_c;  /* size of dim 1; grid z = n * batch_c */
+    uint32_t M, N, K;
+    uint32_t tiles_m, tiles_n;
+    uint32_t pad0, pad1;
+} vx_gemm_args;
+
+/* Block-quantized GEMV / dequantize. */
+typedef struct vx_gemv_args {
+    const uint8_t* w;
+    uint64_t row_stride;   /* bytes between rows of W */
+    const float* x;        /* x[k, b] at x[k*xs_k + b*xs_b] */
+    int64_t xs_k, xs_b;
+    float* y;              /* y[m, b] at y[m*ys_m + b*ys_b] */
+    int64_t ys_m, ys_b;
+    uint32_t M, K, B;      /* B = batch columns handled by this launch */
+    uint32_t nunits;       /* K / 64 (units of 64 weights) */
+    uint32_t chunk_units;  /* units staged in LDS per chunk */
+    uint32_t upitch;       /* LDS pitch (in float4) of one unit-column, odd */
+    uint32_t x_vec;        /* 1: x has stride 1 along K and 16-byte aligned rows */
+    uint32_t pad0;
+} vx_gemv_args;
+
+/* f32 GEMV (the N == 1 route of the GEMM op): y[m] = sum_k A[m,k] x[k]. */
+typedef struct vx_gemv_f32_args {
+    const float* a;
+    int64_t as_m, as_k;
+    const float* x;
+    int64_t xs_k;
+    float* y;
+    int64_t ys_m;
+    uint32_t M, K;
+    uint32_t batch_c;
+    uint32_t pad0;
+    int64_t a_bs[2], x_bs[2], y_bs[2]; /* batch strides (dims n, c) */
+} vx_gemv_f32_args;
+
+#endif /* VX_KARGS_H */
