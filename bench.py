@@ -1,0 +1,250 @@
+"""Benchmark of the vortx linalg hot path on one MI355X.
+
+Headline (BASELINE.json metric, first named config): Q4_0 GEMV y = W x,
+W 11008 x 4096, batch 1, throughput in GB/s of algorithmic bytes
+(M * K/32 * 18 + 4 K + 4 M per launch). One step = one GEMV launch over the
+next of >= 512 MB of distinct weight copies (so the 256 MB Infinity Cache
+cannot serve them), inputs resident in HBM before timing starts.
+
+Secondary lines in the same JSON object: Q8_0 GEMV 4096 x 4096 b=1 (GB/s)
+and the f32 GEMM 4096^3 (TFLOP/s), each with its roofline, plus CPU
+baselines from the oracle's OpenMP restatements on the host cores.
+
+Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
+(captured eager launches) between two synchronizations (wall clock).
+`roofline.achieved` divides the algorithmic bytes (or flops) of one launch
+by the kernel's average launch duration: HIP events recorded on the stream
+the kernels run on, bracketing the same timed region, divided by the number
+of launches. rocprofv3 summaries of the same command are kept under
+profiles/.
+
+Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, public spec
+F32_MFMA_PEAK_TFS = 157.3   # MI355X dense f32 matrix, public spec
+METRIC = "Q4_0/Q8_0 GEMV HBM GB/s at 11008x4096 b=1; f32 GEMM TFLOP/s at 4096^3"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(qtype: int, M: int, K: int, B: int) -> int:
+    from vortx_amd.synthetic import row_bytes
+    return M * row_bytes(qtype, K) + 4 * B * K + 4 * B * M
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/*.json)."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    return None
+
+
+def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str):
+    import torch
+
+    import vortx_amd as vx
+    from vortx_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    nbytes = M * S.row_bytes(qtype, K)
+    ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
+    log(f"[{label}] generating {ncopy} weight copies ({ncopy * nbytes / 2**20:.0f} MiB)")
+    distinct = [S.quant_weights(qtype, M, K, seed=100 + i, device=dev) for i in range(min(4, ncopy))]
+    ws = [distinct[i % len(distinct)].clone() for i in range(ncopy)]
+    del distinct
+    x = S.activations(B, K, seed=7, device=dev)
+    y = torch.empty((B, M), device=dev)
+    g = vx.QuantGemv(0)
+    qws = [vx.QWeight(w, qtype, M, K) for w in ws]
+    xv, yv = x.t(), y.t()
+
+    for i in range(warmup):
+        g.dispatch(yv, qws[i % ncopy], xv)
+    torch.cuda.synchronize()
+
+    # K launches captured once into a HIP graph (chunks of <= 500 nodes) on
+    # stream s and replayed; HIP events on s bracket the timed region, so
+    # their elapsed time / launches is the average launch duration of the
+    # kernel (back-to-back in one stream, gaps included).
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    chunk = min(steps, 500)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(chunk):
+                g.dispatch(yv, qws[i % ncopy], xv, stream=s)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // chunk)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    done = reps * chunk
+    avg_launch_ms = e0.elapsed_time(e1) / done
+    alg = gemv_bytes(qtype, M, K, B)
+    return {
+        "steps": done,
+        "ms_per_step": wall * 1e3 / done,
+        "value": alg * done / wall / 1e9,
+        "avg_launch_ms": avg_launch_ms,
+        "alg_bytes": alg,
+        "weight_copies": ncopy,
+    }
+
+
+def time_gemm(M: int, N: int, K: int, steps: int, warmup: int):
+    import torch
+
+    import vortx_amd as vx
+    from vortx_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    a = S.uniform((M, K), 1, dev)
+    b = S.uniform((K, N), 2, dev)
+    c = torch.empty((M, N), device=dev)
+    gm = vx.Gemm(0)
+    for _ in range(warmup):
+        gm.dispatch(c, a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        gm.dispatch(c, a, b)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = e0.elapsed_time(e1) / steps
+    flops = 2.0 * M * N * K
+    return {"value": flops * steps / wall / 1e12, "avg_launch_ms": launch_ms, "flops": flops,
+            "ms_per_step": wall * 1e3 / steps}
+
+
+def cpu_baselines(threads: int):
+    """Oracle OpenMP restatements on the host cores (bounded samples)."""
+    import numpy as np
+
+    from oracle import oracle as O
+    from vortx_amd import synthetic as S
+
+    out = {}
+    M, K = 11008, 4096
+    w = S.quant_weights(O.Q4_0, M, K, seed=100).numpy()
+    x = S.activations(1, K, seed=7).numpy()
+    O.gemv_q_f32_omp(O.Q4_0, w, M, K, x, threads)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < 10.0:
+        O.gemv_q_f32_omp(O.Q4_0, w, M, K, x, threads)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    out["q4_0"] = {"value": gemv_bytes(2, M, K, 1) / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+                   "sample": f"{n} x Q4_0 GEMV 11008x4096 b=1 on one 25 MB matrix (oracle gemv_q_f32_omp, "
+                             f"builder's dequant-dot restatement; the reference has no quantized path)"}
+    a = np.random.default_rng(1).uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    b = np.random.default_rng(2).uniform(-1, 1, (1024, 1024)).astype(np.float32)
+    for _ in range(3):  # examples/gemm_bench.rs:11-12: 3 warmup + 10 timed
+        O.gemm_tiled_f32_omp(a, b, threads)
+    t0 = time.perf_counter()
+    for _ in range(10):
+        O.gemm_tiled_f32_omp(a, b, threads)
+    dt = (time.perf_counter() - t0) / 10
+    out["gemm1024"] = {"value": 2.0 * 1024 ** 3 / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                       "sample": "10 timed (3 warmup) f32 GEMM 1024^3, OpenMP restatement of gemm_tiled "
+                                 "(64x64x16 tiles, reference k order)"}
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the hot path shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    q40 = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0")
+    log(f"[q4_0] {q40}")
+    q80 = time_gemv(8, 4096, 4096, 1, args.steps, args.warmup, "q8_0")
+    log(f"[q8_0] {q80}")
+    gsteps = max(5, min(50, args.steps // 40))
+    gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
+    log(f"[gemm] {gemm}")
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    cpu = None if args.no_cpu else cpu_baselines(threads)
+    if cpu:
+        log(f"[cpu] {cpu}")
+
+    def roof_hbm(r, name):
+        achieved = r["alg_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(name)}
+
+    gemm_ach = gemm["flops"] / (gemm["avg_launch_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": q40["value"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": q40["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": q40["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "Q4_0 GEMV y=Wx, W 11008x4096 (GGML Q4_0 blocks), batch 1",
+                   "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
+                   "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches"},
+        "roofline": roof_hbm(q40, "gemv_q4_0_11008x4096_b1"),
+        "cpu_baseline": cpu["q4_0"] if cpu else None,
+        "secondary": [
+            {"workload": "Q8_0 GEMV 4096x4096 batch 1", "value": q80["value"], "unit": "GB/s",
+             "ms_per_step": q80["ms_per_step"], "roofline": roof_hbm(q80, "gemv_q8_0_4096x4096_b1")},
+            {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
+             "ms_per_step": gemm["ms_per_step"],
+             "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                          "frac": gemm_ach / F32_MFMA_PEAK_TFS, "traffic": load_traffic("gemm_f32_4096")},
+             "cpu_baseline": cpu["gemm1024"] if cpu else None},
+        ],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
