@@ -90,17 +90,17 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
             for i in range(chunk):
                 g.dispatch(yv, qws[i % ncopy], xv, stream=s)
     torch.cuda.synchronize()
-    graph.replay()
-    torch.cuda.synchronize()
     reps = max(1, steps // chunk)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(s)
-    for _ in range(reps):
+    with torch.cuda.stream(s):  # replay() launches on the current stream
         graph.replay()
-    e1.record(s)
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     done = reps * chunk
     avg_launch_ms = e0.elapsed_time(e1) / done

@@ -74,6 +74,10 @@ def lib() -> C.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
                 "(there is no non-HIP fallback)")
+        # torch ships its own libamdhip64.so.7 (same SONAME as ROCm's). Load it
+        # first so this library binds to the HIP runtime torch already uses:
+        # two runtimes in one process do not see the same devices.
+        import torch  # noqa: F401
         L = C.CDLL(LIB_PATH)
         for name, res, args in SIGNATURES:
             fn = getattr(L, name)

@@ -473,6 +473,176 @@ __device__ __forceinline__ void vx_gemv_bn(const vx_gemv_args& a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Batched path on the matrix cores: v_mfma_f32_16x16x4f32 with
+//   A = 16 rows x 4 k of exactly decoded f32 weights (lane l: row l%16,
+//       k-slot l/16),
+//   B = 4 k x 16 batch columns of f32 x from LDS (lane l: k-slot l/16,
+//       column l%16; columns >= B read zeros),
+//   D = 16 rows x 16 columns in 4 VGPRs (lane l: rows 4(l/16)+v, column
+//       l%16),
+// so weights, x and the accumulation stay f32 and no per-block rescale is
+// needed. A wave owns 16-row tiles; within one MFMA the four k-slots take
+// element s of four consecutive units (64-weight groups) of the same rows, so
+// lane (r, q) streams unit 4g+q of row r with the same 128-bit loads as the
+// batch-1 kernel. KS waves of a workgroup split K (interleaved unit
+// groups) and their partial tiles are summed through LDS at the end; x is
+// staged per K chunk as [column][k] with a pitch of Kc + 4 floats (bank
+// conflict free for the 16 columns a 16-lane phase reads).
+template <int QT>
+__device__ __forceinline__ void vx_unit_decode64(const uint32_t (&r)[vx_unit<QT>::NW], uint32_t u, float (&w)[64]) {
+    if constexpr (QT == VX_Q4_0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
+            const float o = -8.f * d;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t qd = h ? r[5 + i] : __builtin_amdgcn_alignbit(r[i + 1], r[i], 16);
+                const uint32_t lo = vx_and(qd, 0x0F0F0F0Fu), hi = vx_and(qd >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    w[32 * h + 4 * i + b] = __builtin_fmaf(vx_ub(lo, b), d, o);
+                    w[32 * h + 16 + 4 * i + b] = __builtin_fmaf(vx_ub(hi, b), d, o);
+                }
+            }
+        }
+    } else if constexpr (QT == VX_Q8_0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
+            const float o = -128.f * d;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t qd = h ? r[9 + i] : __builtin_amdgcn_alignbit(r[i + 1], r[i], 16);
+                const uint32_t uq = vx_xor(qd, 0x80808080u);  // q + 128, exact: (q+128) d - 128 d
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w[32 * h + 4 * i + b] = __builtin_fmaf(vx_ub(uq, b), d, o);
+            }
+        }
+    } else {
+        float sc[4];
+        vx_unit_scales<QT>(r, u, sc);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = vx_and(r[4 + i], 0x0F0F0F0Fu), hi = vx_and(r[4 + i] >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[4 * i + b] = __builtin_fmaf(vx_ub(lo, b), sc[0], sc[1]);
+                w[32 + 4 * i + b] = __builtin_fmaf(vx_ub(hi, b), sc[2], sc[3]);
+            }
+        }
+    }
+}
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// One 16-row tile per wave. The wave's unit groups (256 k each) are
+// g = ks, ks + KS, ...; their weights are loaded PD groups ahead in a
+// register ring, across LDS chunk boundaries, so HBM latency overlaps the
+// MFMA work. kc / 256 (groups per chunk) is a multiple of KS, so all waves
+// of a workgroup cross chunk boundaries - and reach the staging barriers -
+// at the same loop step.
+template <int QT, int KS, int PD>
+__device__ __forceinline__ void vx_gemv_mfma(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    constexpr int TG = 4 / KS;  // tiles per workgroup
+    float* xs = (float*)vx_lds_x;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t i16 = lane & 15u, q = lane >> 4;
+    const uint32_t ks = wave % KS;
+    const uint32_t tile = blockIdx.x * TG + wave / KS;
+    const uint32_t kc = a.chunk_units * 64u;  // k per LDS chunk, multiple of 256 * KS
+    const uint32_t pitch = kc + 4u;
+    const uint32_t ngroups = a.K / 256u;
+    const uint32_t nj = ngroups > ks ? (ngroups - ks + KS - 1) / KS : 0u;  // this wave's groups
+    const uint32_t row = min(tile * 16u + i16, a.M - 1u);  // rows past M read the last row
+    const uint8_t* wrow = a.w + (uint64_t)row * a.row_stride;
+
+    f32x4v acc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t wr[PD][NW];
+#pragma unroll
+    for (int p = 0; p < PD; ++p) {
+        const uint32_t g = ks + KS * min((uint32_t)p, nj ? nj - 1u : 0u);
+        vx_load_unit<QT>(wrow, 4u * min(g, ngroups - 1u) + q, wr[p]);
+    }
+
+    uint32_t cur_chunk = 0xFFFFFFFFu;
+    // every wave runs the same number of outer steps (the max over waves) so
+    // the staging barriers line up; steps past a wave's last group skip work.
+    const uint32_t nj_max = (ngroups + KS - 1) / KS;
+    for (uint32_t j0 = 0; j0 < nj_max; j0 += PD) {
+#pragma unroll
+        for (int p = 0; p < PD; ++p) {
+            const uint32_t j = j0 + p;
+            if (j >= nj_max) break;  // uniform across the workgroup
+            const uint32_t g = ks + KS * j;
+            const uint32_t chunk = (KS * j * 256u) / kc;  // same for every ks
+            if (chunk != cur_chunk) {
+                cur_chunk = chunk;
+                const uint32_t k0 = chunk * kc;
+                const uint32_t klen = min(kc, a.K - k0);
+                __syncthreads();
+                for (uint32_t f = threadIdx.x; f < 16u * (kc / 4u); f += VX_WG) {
+                    const uint32_t b = f / (kc / 4u), k4 = 4u * (f % (kc / 4u));
+                    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (b < a.B && k4 < klen) {
+                        const int64_t k = (int64_t)k0 + k4;
+                        if (a.x_vec) {
+                            v = *(const f32x4*)(a.x + b * a.xs_b + k);
+                        } else {
+                            const float* xp = a.x + b * a.xs_b + k * a.xs_k;
+                            v = f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+                        }
+                    }
+                    *(f32x4*)(xs + b * pitch + k4) = v;
+                }
+                __syncthreads();
+            }
+            if (j < nj) {
+                float w[64];
+                vx_unit_decode64<QT>(wr[p], 4u * g + q, w);
+                // prefetch the group PD steps ahead into the freed slot
+                const uint32_t jn = min(j + PD, nj - 1u);
+                vx_load_unit<QT>(wrow, 4u * (ks + KS * jn) + q, wr[p]);
+                const float* xb = xs + i16 * pitch + (g * 256u - chunk * kc) + 64u * q;
+#pragma unroll
+                for (int s4 = 0; s4 < 16; ++s4) {
+                    const f32x4 xv = *(const f32x4*)(xb + 4 * s4);
+                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 0], xv.x, acc[0], 0, 0, 0);
+                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 1], xv.y, acc[1], 0, 0, 0);
+                    acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 2], xv.z, acc[2], 0, 0, 0);
+                    acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 3], xv.w, acc[3], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // Sum the accumulators, then the KS partial tiles through LDS; store
+    // rows 4(l/16)+v, column l%16.
+    f32x4v tot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    if constexpr (KS > 1) {
+        __syncthreads();
+        f32x4v* red = (f32x4v*)vx_lds_x;  // [wave][lane]
+        red[wave * 64 + lane] = tot;
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int o = 1; o < KS; ++o) tot += red[(wave + o) * 64 + lane];
+        }
+    }
+    if (ks == 0 && i16 < a.B) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t r = tile * 16u + 4u * q + v;
+            if (r < a.M) a.y[(int64_t)r * a.ys_m + (int64_t)i16 * a.ys_b] = tot[v];
+        }
+    }
+}
+
 // Any layout fallback (K a multiple of 32, any alignment, any B): one
 // wave per row, lane l decodes 32-weight groups l, l+64, ... byte by byte.
 template <int QT>
@@ -526,6 +696,10 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
         if (a.x_vec) vx_gemv_bn<QT, NB, R, LPR, true>(a);                                         \
         else vx_gemv_bn<QT, NB, R, LPR, false>(a);                                                \
     }
+#define VX_GEMV_MFMA(QT, QN, KS, PD)                                                              \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_mfma_##QN##_s##KS##_p##PD(vx_gemv_args a) { \
+        vx_gemv_mfma<QT, KS, PD>(a);                                                              \
+    }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
     VX_GEMV_B1(QT, QN, 2)                                                                           \
@@ -539,6 +713,12 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     VX_GEMV_BN(QT, QN, 4, 2, 64)                                                                    \
     VX_GEMV_BN(QT, QN, 8, 2, 32)                                                                    \
     VX_GEMV_BN(QT, QN, 16, 2, 16)                                                                   \
+    VX_GEMV_MFMA(QT, QN, 1, 2)                                                                      \
+    VX_GEMV_MFMA(QT, QN, 2, 2)                                                                      \
+    VX_GEMV_MFMA(QT, QN, 4, 2)                                                                      \
+    VX_GEMV_MFMA(QT, QN, 1, 4)                                                                      \
+    VX_GEMV_MFMA(QT, QN, 2, 4)                                                                      \
+    VX_GEMV_MFMA(QT, QN, 4, 4)                                                                      \
     extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_generic_##QN(vx_gemv_args a) {     \
         vx_gemv_generic<QT>(a);                                                                     \
     }                                                                                               \

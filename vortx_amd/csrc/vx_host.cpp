@@ -4,7 +4,7 @@
 // Runtime: the gfx950 code objects built by hipcc --genco are embedded in
 // this library (vx_embed.S); vx_init loads them with hipModuleLoadData and
 // resolves every kernel once; launches go through hipModuleLaunchKernel with
-// the kernel's argument struct (vx_kargs.h) passed by value.
+// the kernel's argument struct (vx_kargs.h) passed by value (kernelParams).
 //
 // Ops: Gemm::dispatch / dispatch_naive / dispatch_tiled of
 // src/linalg/gemm.rs:47-305 (canonicalize, validate, pick a kernel, grid)
@@ -91,15 +91,18 @@ struct DeviceGuard {
     }
 };
 
+// Every kernel takes one argument: its vx_*_args struct by value. It is
+// passed through kernelParams (an array of pointers to each argument), which
+// the runtime copies by the kernel's argument layout at launch, and which
+// stream capture copies into the graph node, so the struct may live on this
+// stack frame.
 template <class Args>
 static int launch(vx_ctx ctx, int k, dim3 grid, dim3 block, size_t lds, vx_stream stream, const Args& args) {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return VX_OK;
     Args copy = args;
-    size_t size = sizeof(Args);
-    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, &copy, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
-                      HIP_LAUNCH_PARAM_END};
+    void* params[] = {&copy};
     const hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid.x, grid.y, grid.z, block.x, block.y, block.z,
-                                               (unsigned)lds, (hipStream_t)stream, nullptr, config);
+                                               (unsigned)lds, (hipStream_t)stream, params, nullptr);
     if (e != hipSuccess) return fail_hip(e, kKernelNames[k]);
     return VX_OK;
 }
@@ -367,6 +370,17 @@ static int bn_kernel(uint32_t qt, int NB) {
     return tab[q_index(qt)][ni];
 }
 
+static int mfma_kernel(uint32_t qt, int ks, int pd) {
+    static const int tab[3][2][3] = {
+        {{K_vx_gemv_mfma_q4_0_s1_p2, K_vx_gemv_mfma_q4_0_s2_p2, K_vx_gemv_mfma_q4_0_s4_p2},
+         {K_vx_gemv_mfma_q4_0_s1_p4, K_vx_gemv_mfma_q4_0_s2_p4, K_vx_gemv_mfma_q4_0_s4_p4}},
+        {{K_vx_gemv_mfma_q8_0_s1_p2, K_vx_gemv_mfma_q8_0_s2_p2, K_vx_gemv_mfma_q8_0_s4_p2},
+         {K_vx_gemv_mfma_q8_0_s1_p4, K_vx_gemv_mfma_q8_0_s2_p4, K_vx_gemv_mfma_q8_0_s4_p4}},
+        {{K_vx_gemv_mfma_q4_k_s1_p2, K_vx_gemv_mfma_q4_k_s2_p2, K_vx_gemv_mfma_q4_k_s4_p2},
+         {K_vx_gemv_mfma_q4_k_s1_p4, K_vx_gemv_mfma_q4_k_s2_p4, K_vx_gemv_mfma_q4_k_s4_p4}}};
+    return tab[q_index(qt)][pd == 4 ? 1 : 0][ks == 1 ? 0 : ks == 2 ? 1 : 2];
+}
+
 static int generic_kernel(uint32_t qt) {
     return qt == VX_Q4_0 ? K_vx_gemv_generic_q4_0 : qt == VX_Q8_0 ? K_vx_gemv_generic_q8_0 : K_vx_gemv_generic_q4_k;
 }
@@ -429,6 +443,45 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
 
     const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
+    const char* bmode = std::getenv("VX_GEMV_BATCHED");
+    const bool use_mfma = fast && K % 256 == 0 && !(bmode && std::strcmp(bmode, "simt") == 0);
+    if (B >= 2 && use_mfma) {
+        // Matrix-core path: up to 16 batch columns per launch, f32 MFMA.
+        const uint32_t ntiles = (M + 15u) / 16u;
+        int ks = 4;
+        for (int c : {1, 2, 4})
+            if ((uint64_t)ntiles * c / 4u >= (uint64_t)ctx->num_cus * 13u / 10u) {
+                ks = c;
+                break;
+            }
+        if (const char* e = std::getenv("VX_MFMA_KS")) {
+            const int v = std::atoi(e);
+            if (v == 1 || v == 2 || v == 4) ks = v;
+        }
+        int pd = 4;
+        if (const char* e = std::getenv("VX_MFMA_PD")) pd = std::atoi(e) == 2 ? 2 : 4;
+        // k per LDS chunk (16 columns x (kc + 4) floats): a multiple of 256 * ks
+        const uint32_t step = 256u * (uint32_t)ks;
+        uint32_t kc = 1024u > step ? 1024u : step;
+        if (const char* e = std::getenv("VX_MFMA_KC")) kc = ((uint32_t)std::atoi(e) / step) * step;
+        if (kc < step) kc = step;
+        while (kc > step && (size_t)16u * (kc + 4u) * 4u > budget) kc -= step;
+        if ((size_t)16u * (kc + 4u) * 4u > budget) return fail(VX_ERR_UNSUPPORTED, "LDS budget too small");
+        const uint32_t tg_per_wg = 4u / (uint32_t)ks;
+        const uint32_t grid = (ntiles + tg_per_wg - 1) / tg_per_wg;
+        const size_t lds = (size_t)16u * (kc + 4u) * 4u;
+        for (uint32_t b0 = 0; b0 < B; b0 += 16) {
+            a.B = B - b0 < 16 ? B - b0 : 16;
+            a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
+            a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
+            a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
+            a.chunk_units = kc / 64u;
+            a.upitch = 0;
+            s = launch(ctx, mfma_kernel(w->qtype, ks, pd), dim3(grid), dim3(VX_WG), lds, stream, a);
+            if (s) return s;
+        }
+        return VX_OK;
+    }
     uint32_t b0 = 0;
     while (b0 < B) {
         const uint32_t rem = B - b0;

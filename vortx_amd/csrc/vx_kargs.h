@@ -2,8 +2,8 @@
  * vx_kargs.h — kernel argument blocks shared by the host library (g++)
  * and the gfx950 kernels (hipcc). Each kernel takes one of these structs
  * by value; the host passes it to hipModuleLaunchKernel through
- * HIP_LAUNCH_PARAM_BUFFER_POINTER, so the layout must be identical on both
- * sides: only fixed-width integers and pointers, naturally aligned.
+ * kernelParams, so the layout must be identical on both sides: only
+ * fixed-width integers and pointers, naturally aligned.
  */
 #ifndef VX_KARGS_H
 #define VX_KARGS_H
