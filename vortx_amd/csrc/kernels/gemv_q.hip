@@ -151,6 +151,143 @@ __device__ __forceinline__ void vx_gemv_b1(const vx_gemv_args& a) {
 }
 
 // ------------------------------------------------------------------------
+// Batch 1, persistent: one workgroup of WGT threads per CU (grid = CU
+// count), wave w of the chip owning rows w, w + W, w + 2W, ... (W = waves
+// in the grid). Items (row, pass of 64 units) stream through a P-deep
+// register ring.
+// Ordering is what makes this fast. x is needed before any arithmetic, an
+// x request queued behind the CU's weight requests waits for them, and a
+// wave issuing weight loads stalls while the CU's memory queue is full.
+// So: every wave issues its share of the x loads; a bare s_barrier (no
+// wait) puts all x requests of the CU ahead of every weight request; each
+// wave issues one weight item only, stores x to LDS as soon as x alone has
+// arrived and reaches the one barrier before any wave can stall on a full
+// queue; the rest of the ring is issued after it. The two 32-block sums of
+// x per unit (for the offset terms of vx_unit_dot_b1) are reduced in the
+// staging step with lane shuffles, so no second barrier is needed.
+// WGT = 1024: 16 waves of at most 128 VGPRs; 512: 8 waves with room for a
+// deeper ring. x must fit VX_P_XF float4 (K <= 16384).
+#define VX_P_XF 4096u
+
+template <int QT, int P, int WGT, bool XV>
+__device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    constexpr int XPT = (int)(VX_P_XF / WGT);
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    // wave-uniform (scalar) so that the item loop runs on scalar branches
+    // and the wait counts stay exact
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nwv = gridDim.x * (WGT / 64u);
+    const uint32_t gw = blockIdx.x * (WGT / 64u) + wave;
+    const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
+    const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
+    const uint32_t nitems = nrows * npass;
+    const uint32_t upitch = a.upitch;
+    float* sxs = (float*)(vx_lds_x + 16u * upitch);  // [unit][2]
+
+    // 1. x loads: float4 f of x = slot f & 15 of unit f >> 4 (k = 4 f).
+    const uint32_t total = nunits * 16u;
+    f32x4 xr[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        if ((uint32_t)i * WGT >= total) break;  // uniform: rounds past x
+        const uint32_t f = min(t + WGT * (uint32_t)i, total - 1u);
+        if constexpr (XV) {
+            xr[i] = *(const f32x4*)(a.x + 4 * (int64_t)f);
+        } else {
+            const float* xp = a.x + 4 * (int64_t)f * a.xs_k;
+            xr[i] = f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+        }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    // 2. the first item (clamped: past the end an item repeats the last
+    //    one, which the cache serves; y is written only for real rows).
+    const uint8_t* wbase = a.w;
+    auto item_ptr = [&](uint32_t it, uint32_t& unit) {
+        const uint32_t c = nitems ? min(it, nitems - 1u) : 0u;
+        const uint32_t ri = c / npass, p = c - ri * npass;
+        const uint32_t row = min(gw + ri * nwv, a.M - 1u);
+        unit = min(64u * p + lane, nunits - 1u);
+        return wbase + (uint64_t)row * a.row_stride;
+    };
+    uint32_t wr[P][NW];
+    {
+        uint32_t u;
+        const uint8_t* rp = item_ptr(0u, u);
+        vx_load_unit<QT>(rp, u, wr[0]);
+    }
+
+    // 3. x to LDS (waits for the x loads only) with the per-unit sums:
+    //    the 16 slots of a unit sit in 16 consecutive lanes.
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        if ((uint32_t)i * WGT >= total) break;
+        const uint32_t f = t + WGT * (uint32_t)i;
+        const bool in = f < total;
+        float ps = in ? (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w) : 0.f;
+        ps += __shfl_xor(ps, 1, 64);
+        ps += __shfl_xor(ps, 2, 64);
+        ps += __shfl_xor(ps, 4, 64);
+        if (in) {
+            vx_lds_x[(f & 15u) * upitch + (f >> 4)] = xr[i];
+            if ((f & 7u) == 0u) sxs[2u * (f >> 4) + ((f >> 3) & 1u)] = ps;
+        }
+    }
+    __syncthreads();
+
+    // 4. the rest of the ring, then stream the items. The main loop runs
+    //    whole rounds of P items so that every path through it issues the
+    //    same loads (exact wait counts); the last partial round follows.
+#pragma unroll
+    for (int j = 1; j < P; ++j) {
+        uint32_t u;
+        const uint8_t* rp = item_ptr((uint32_t)j, u);
+        vx_load_unit<QT>(rp, u, wr[j]);
+    }
+    float xv[64];
+    float sx0 = 0.f, sx1 = 0.f;
+    uint32_t cur = ~0u;
+    float acc = 0.f;
+    auto body = [&](uint32_t it, uint32_t (&w)[NW]) {
+        const uint32_t ri = it / npass, p = it - ri * npass;
+        const uint32_t u = 64u * p + lane;
+        const bool act = u < nunits;
+        const uint32_t us = act ? u : nunits - 1u;
+        if (p != cur) {
+            cur = p;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const f32x4 v = vx_lds_x[q * upitch + us];
+                xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
+            }
+            sx0 = sxs[2u * us];
+            sx1 = sxs[2u * us + 1u];
+        }
+        const float d = vx_unit_dot_b1<QT>(w, xv, sx0, sx1, us);
+        acc += act ? d : 0.f;
+        uint32_t nu;
+        const uint8_t* rp = item_ptr(it + P, nu);
+        vx_load_unit<QT>(rp, nu, w);
+        if (p == npass - 1u) {
+            const float sum = vx_wave_sum(acc);
+            if (lane == 0) a.y[(int64_t)(gw + ri * nwv) * a.ys_m] = sum;
+            acc = 0.f;
+        }
+    };
+    const uint32_t nfull = nitems - nitems % P;
+    for (uint32_t it0 = 0; it0 < nfull; it0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) body(it0 + (uint32_t)j, wr[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < P - 1; ++j)
+        if (nfull + (uint32_t)j < nitems) body(nfull + (uint32_t)j, wr[j]);
+}
+
+// ------------------------------------------------------------------------
 // Integer-dot path. During staging every 32-element block of x (per batch
 // column) is split into two int8 levels with one f32 scale:
 //     x ~= c * (254 * x1 + x2),   c = max|x_blk| / (127 * 254),
@@ -643,6 +780,223 @@ __device__ __forceinline__ void vx_gemv_mfma(const vx_gemv_args& a) {
     }
 }
 
+// ------------------------------------------------------------------------
+// Batched path on f16 matrix cores at f32 accuracy (B >= 2, 16 columns per
+// launch).
+//   D[i][j] = sum_k X[i][k] Wq[k][j] with v_mfma_f32_16x16x32_f16:
+//     Wq (B operand) = the block integers of 16 rows j (q - 8 for Q4_0, q
+//       for Q8_0 and Q4_K), exact in f16: nibbles / bytes are placed in the
+//       mantissa of 1024.0 and the offset is removed with an exact packed
+//       f16 subtraction;
+//     X (A operand) = 16 batch columns i of x in two f16 levels x1 + x2.
+//       Per chunk of 512 k and column, x is first scaled by 2^n so that the
+//       chunk's max |x| lies in [2^14, 2^15): then |x s - x1 - x2| <=
+//       max(2^-22 |x s|, 2^-25), i.e. finer than f32 rounding relative to
+//       the column's scale, with no f16 overflow or loss to subnormals;
+//   each level is one MFMA into the block's accumulator, and the lane that
+//   loaded row j applies the block scale: acc += d D (Q4_K: + (-dmin m) S,
+//   S the scaled block sum of x). At the end of a chunk acc_chunk * 2^-n is
+//   added to the running sum.
+// Lane l: row j = l%16 of the tile, k-octet o = l/16 of every 32-block
+//   (A and B operands), outputs D[4o+v][j] = y[row j][column 4o+v].
+// The four lanes of a row load the same 64-weight unit (the TA merges the
+// identical addresses) and each takes one octet of every block. Within an
+// octet, k follows the order in which the packing yields the pairs:
+//   (e0,e2) (e1,e3) (e4,e6) (e5,e7) of the octet's 8 elements, where
+//   Q4_0's octet o is elements 4o..4o+3 and 16+4o..16+4o+3 of its block
+//   (low and high nibbles of qs dword o), and Q8_0 / Q4_K's octet is
+//   elements 8o..8o+7.
+// LDS: per 32-block, level and octet, 16 columns x 16 bytes (lane l reads
+//   group (o, l%16): conflict free); then the Q4_K block sums [blk][col],
+//   the per-wave column maxima and the chunk exponents.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4h __attribute__((ext_vector_type(4)));
+
+#define VX_H_KC 512u  // k per staged chunk
+#define VX_H_NG (VX_H_KC / 128u)  // 8-element groups per thread per chunk
+
+// Exact packed f16 subtraction of a small-integer offset from 1024 + q pairs.
+__device__ __forceinline__ uint32_t vx_h2_sub(uint32_t bits, float off) {
+    const _Float16 o = (_Float16)off;
+    const f16x2 v = __builtin_bit_cast(f16x2, bits) - f16x2{o, o};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// f16 pairs (1024 + nibble) of the nibbles at bits (sh, sh + 16) of w.
+__device__ __forceinline__ uint32_t vx_nib_pair(uint32_t w, uint32_t sh) {
+    return ((w >> sh) & 0x000F000Fu) | 0x64006400u;
+}
+
+// x of one 8-element group (block blk, octet o, column col) of the chunk at
+// k0, in packing order. Q4_0 groups are two float4 at 4o and 16 + 4o, the
+// others at 8o and 8o + 4.
+template <int QT, int XV>
+__device__ __forceinline__ void vx_h_load(const vx_gemv_args& a, uint32_t k0, uint32_t blk, uint32_t o,
+                                          uint32_t col, bool live, float (&e)[8]) {
+    const uint32_t ka = k0 + blk * 32u + (QT == VX_Q4_0 ? 4u * o : 8u * o);
+    const uint32_t kb = ka + (QT == VX_Q4_0 ? 16u : 4u);
+    if constexpr (XV) {
+        f32x4 u = f32x4{0.f, 0.f, 0.f, 0.f}, v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            const float* xc = a.x + (int64_t)col * a.xs_b;
+            u = *(const f32x4*)(xc + ka);
+            v = *(const f32x4*)(xc + kb);
+        }
+        e[0] = u.x; e[1] = u.z; e[2] = u.y; e[3] = u.w;
+        e[4] = v.x; e[5] = v.z; e[6] = v.y; e[7] = v.w;
+    } else {
+        const uint32_t ord[4] = {0u, 2u, 1u, 3u};
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t k = (t < 4 ? ka : kb) + ord[t & 3];
+            e[t] = live ? a.x[(int64_t)col * a.xs_b + (int64_t)k * a.xs_k] : 0.f;
+        }
+    }
+}
+
+template <int QT, int KS, int XV>
+__device__ __forceinline__ void vx_gemv_h16(const vx_gemv_args& a) {
+    constexpr int TG = 4 / KS;  // 16-row tiles per workgroup
+    constexpr uint32_t NBLK = VX_H_KC / 32u;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t j16 = lane & 15u, o = lane >> 4;
+    const uint32_t ks = wave % KS;
+    const uint32_t tile = blockIdx.x * TG + wave / KS;
+    const uint32_t row = min(tile * 16u + j16, a.M - 1u);
+    const uint8_t* wrow = a.w + (uint64_t)row * a.row_stride;
+
+    uint4* xg = (uint4*)vx_lds_x;                          // [blk][level][octet][col]
+    float* sums = (float*)(xg + NBLK * 2u * 64u);           // [blk][col] (Q4_K)
+    float* wmax = sums + NBLK * 16u;                        // [wave][col]
+    int* nexp = (int*)(wmax + 64);                          // [col]
+
+    f32x4h acc = f32x4h{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t k0 = 0; k0 < a.K; k0 += VX_H_KC) {
+        const uint32_t klen = min(VX_H_KC, a.K - k0);  // a multiple of 64
+        // ---- stage: load the chunk, per-column max |x|
+        const uint32_t col = t & 15u;
+        float e[VX_H_NG][8];
+        float mx = 0.f;
+#pragma unroll
+        for (uint32_t g = 0; g < VX_H_NG; ++g) {
+            const uint32_t f = t + g * VX_WG;
+            const uint32_t go = (f >> 4) & 3u, blk = f >> 6;
+            vx_h_load<QT, XV>(a, k0, blk, go, col, col < a.B && blk * 32u < klen, e[g]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(e[g][i]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (lane < 16u) wmax[wave * 16u + lane] = mx;
+        __syncthreads();  // also: every wave is done with the previous chunk
+        const float m = fmaxf(fmaxf(wmax[col], wmax[16u + col]), fmaxf(wmax[32u + col], wmax[48u + col]));
+        const int n = (m < __builtin_inff()) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
+        if (t < 16u) nexp[t] = n;
+#pragma unroll
+        for (uint32_t g = 0; g < VX_H_NG; ++g) {
+            const uint32_t f = t + g * VX_WG;
+            const uint32_t go = (f >> 4) & 3u, blk = f >> 6;
+            uint32_t l1[4], l2[4];
+            float part = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i += 2) {
+                const float v0 = __builtin_amdgcn_ldexpf(e[g][i], n), v1 = __builtin_amdgcn_ldexpf(e[g][i + 1], n);
+                part += v0 + v1;
+                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
+                const _Float16 r0 = (_Float16)(v0 - (float)h0), r1 = (_Float16)(v1 - (float)h1);
+                l1[i / 2] = __builtin_bit_cast(uint32_t, f16x2{h0, h1});
+                l2[i / 2] = __builtin_bit_cast(uint32_t, f16x2{r0, r1});
+            }
+            const uint32_t base = blk * 128u + go * 16u + col;
+            xg[base] = uint4{l1[0], l1[1], l1[2], l1[3]};
+            xg[base + 64u] = uint4{l2[0], l2[1], l2[2], l2[3]};
+            if constexpr (QT == VX_Q4_K) {
+                part += __shfl_xor(part, 16, 64);
+                part += __shfl_xor(part, 32, 64);
+                if (go == 0u) sums[blk * 16u + col] = part;
+            }
+        }
+        __syncthreads();
+
+        // ---- compute: units of this wave's k-slice, two 32-blocks each
+        f32x4h accc = f32x4h{0.f, 0.f, 0.f, 0.f};
+        const uint32_t u0 = k0 / 64u, un = klen / 64u;
+        for (uint32_t ul = ks; ul < un; ul += KS) {
+            uint32_t r[vx_unit<QT>::NW];
+            vx_load_unit<QT>(wrow, u0 + ul, r);
+            float sc[4];
+            if constexpr (QT == VX_Q4_K) vx_unit_scales<QT>(r, u0 + ul, sc);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t blk = 2u * ul + h;
+                uint32_t p[4];
+                float d;
+                if constexpr (QT == VX_Q4_0) {
+                    const uint32_t qd = h ? r[5 + o] : __builtin_amdgcn_alignbit(r[o + 1], r[o], 16);
+                    p[0] = vx_h2_sub(vx_nib_pair(qd, 0), 1032.f);
+                    p[1] = vx_h2_sub(vx_nib_pair(qd, 8), 1032.f);
+                    p[2] = vx_h2_sub(vx_nib_pair(qd, 4), 1032.f);
+                    p[3] = vx_h2_sub(vx_nib_pair(qd, 12), 1032.f);
+                    d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
+                } else if constexpr (QT == VX_Q8_0) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) {
+                        const int di = 2 * (int)o + q;
+                        const uint32_t qd = h ? r[9 + di] : __builtin_amdgcn_alignbit(r[di + 1], r[di], 16);
+                        const uint32_t u = vx_xor(qd, 0x80808080u);  // q + 128
+                        p[2 * q] = vx_h2_sub((u & 0x00FF00FFu) | 0x64006400u, 1152.f);
+                        p[2 * q + 1] = vx_h2_sub(((u >> 8) & 0x00FF00FFu) | 0x64006400u, 1152.f);
+                    }
+                    d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
+                } else {
+                    const uint32_t w0 = r[4 + 2 * o], w1 = r[5 + 2 * o], sh = 4u * h;
+                    p[0] = vx_h2_sub(vx_nib_pair(w0, sh), 1024.f);
+                    p[1] = vx_h2_sub(vx_nib_pair(w0, sh + 8u), 1024.f);
+                    p[2] = vx_h2_sub(vx_nib_pair(w1, sh), 1024.f);
+                    p[3] = vx_h2_sub(vx_nib_pair(w1, sh + 8u), 1024.f);
+                    d = sc[2 * h];
+                }
+                const f16x8 bw = __builtin_bit_cast(f16x8, uint4{p[0], p[1], p[2], p[3]});
+                const uint32_t gb = blk * 128u + o * 16u + j16;
+                const f16x8 x1 = __builtin_bit_cast(f16x8, xg[gb]);
+                const f16x8 x2 = __builtin_bit_cast(f16x8, xg[gb + 64u]);
+                f32x4h dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, bw, f32x4h{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(x2, bw, dd, 0, 0, 0);
+                if constexpr (QT == VX_Q4_K) {
+                    const f32x4 sv = *(const f32x4*)(sums + blk * 16u + 4u * o);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) accc[v] = __builtin_fmaf(sc[2 * h + 1], sv[v], accc[v]);
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) accc[v] = __builtin_fmaf(d, dd[v], accc[v]);
+            }
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] += __builtin_amdgcn_ldexpf(accc[v], -nexp[4u * o + v]);
+    }
+    if constexpr (KS > 1) {
+        __syncthreads();
+        f32x4h* red = (f32x4h*)vx_lds_x;
+        red[wave * 64 + lane] = acc;
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int w = 1; w < KS; ++w) acc += red[(wave + w) * 64 + lane];
+        }
+    }
+    if (ks == 0) {
+        const uint32_t r0 = tile * 16u + j16;
+        if (r0 < a.M) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t c = 4u * o + v;
+                if (c < a.B) a.y[(int64_t)r0 * a.ys_m + (int64_t)c * a.ys_b] = acc[v];
+            }
+        }
+    }
+}
+
 // Any layout fallback (K a multiple of 32, any alignment, any B): one
 // wave per row, lane l decodes 32-weight groups l, l+64, ... byte by byte.
 template <int QT>
@@ -700,6 +1054,14 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_mfma_##QN##_s##KS##_p##PD(vx_gemv_args a) { \
         vx_gemv_mfma<QT, KS, PD>(a);                                                              \
     }
+#define VX_GEMV_H16(QT, QN, KS)                                                                 \
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_h16_##QN##_s##KS(vx_gemv_args a) {  \
+        if (a.x_vec) vx_gemv_h16<QT, KS, 1>(a); else vx_gemv_h16<QT, KS, 0>(a);                \
+    }
+#define VX_GEMV_P1(QT, QN, P, WGT)                                                              \
+    extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(vx_gemv_args a) {  \
+        if (a.x_vec) vx_gemv_p1<QT, P, WGT, true>(a); else vx_gemv_p1<QT, P, WGT, false>(a);   \
+    }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
     VX_GEMV_B1(QT, QN, 2)                                                                           \
@@ -713,6 +1075,9 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     VX_GEMV_BN(QT, QN, 4, 2, 64)                                                                    \
     VX_GEMV_BN(QT, QN, 8, 2, 32)                                                                    \
     VX_GEMV_BN(QT, QN, 16, 2, 16)                                                                   \
+    VX_GEMV_H16(QT, QN, 1)                                                                         \
+    VX_GEMV_H16(QT, QN, 2)                                                                         \
+    VX_GEMV_H16(QT, QN, 4)                                                                         \
     VX_GEMV_MFMA(QT, QN, 1, 2)                                                                      \
     VX_GEMV_MFMA(QT, QN, 2, 2)                                                                      \
     VX_GEMV_MFMA(QT, QN, 4, 2)                                                                      \
@@ -727,3 +1092,9 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
 VX_GEMV_ALL(VX_Q4_0, q4_0)
 VX_GEMV_ALL(VX_Q8_0, q8_0)
 VX_GEMV_ALL(VX_Q4_K, q4_k)
+VX_GEMV_P1(VX_Q4_0, q4_0, 2, 1024)
+VX_GEMV_P1(VX_Q8_0, q8_0, 1, 1024)
+VX_GEMV_P1(VX_Q4_K, q4_k, 2, 1024)
+VX_GEMV_P1(VX_Q4_0, q4_0, 4, 512)
+VX_GEMV_P1(VX_Q8_0, q8_0, 3, 512)
+VX_GEMV_P1(VX_Q4_K, q4_k, 4, 512)

@@ -69,6 +69,21 @@ __device__ __forceinline__ float vx_ub(uint32_t v, int b) {
     return (float)((v >> (8 * b)) & 0xFFu);
 }
 
+// The four nibbles at bits (sh, sh+8, sh+16, sh+24) of w as floats scaled
+// by VX_NIB (= 2^-9), two per v_cvt_pk_f32_fp8: a byte 0..15 read as an
+// OCP e4m3 value is exactly q * 2^-9 (subnormals for q < 8, exponent 1
+// for q >= 8), so one packed convert replaces two byte converts.
+#define VX_NIB_INV 512.0f
+__device__ __forceinline__ void vx_nib4(uint32_t w, int sh, float (&o)[4]) {
+    const uint32_t b = vx_and(sh ? (w >> 4) : w, 0x0F0F0F0Fu);
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(b, false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(b, true);
+    o[0] = lo[0];
+    o[1] = lo[1];
+    o[2] = hi[0];
+    o[3] = hi[1];
+}
+
 template <int QT> struct vx_unit;
 template <> struct vx_unit<VX_Q4_0> { static constexpr int NW = 9;  static constexpr int QK = 32;  static constexpr int BB = 18; };
 template <> struct vx_unit<VX_Q8_0> { static constexpr int NW = 17; static constexpr int QK = 32;  static constexpr int BB = 34; };
@@ -146,17 +161,18 @@ __device__ __forceinline__ float vx_unit_dot_b1(const uint32_t (&r)[vx_unit<QT>:
             float slo = 0.f, shi = 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = vx_and(q[4 * h + i], 0x0F0F0F0Fu);
-                const uint32_t hi = vx_and(q[4 * h + i], 0xF0F0F0F0u);  // 16 * nibble per byte
+                float wl[4], wh[4];
+                vx_nib4(q[4 * h + i], 0, wl);
+                vx_nib4(q[4 * h + i], 4, wh);
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
-                    slo = __builtin_fmaf(vx_ub(lo, b), xv[32 * h + 4 * i + b], slo);
-                    shi = __builtin_fmaf(vx_ub(hi, b), xv[32 * h + 16 + 4 * i + b], shi);
+                    slo = __builtin_fmaf(wl[b], xv[32 * h + 4 * i + b], slo);
+                    shi = __builtin_fmaf(wh[b], xv[32 * h + 16 + 4 * i + b], shi);
                 }
             }
             const float d = h ? d1 : d0;
             const float sx = h ? sx1 : sx0;
-            res = __builtin_fmaf(d, __builtin_fmaf(shi, 0.0625f, slo) - 8.f * sx, res);
+            res = __builtin_fmaf(d, __builtin_fmaf(slo + shi, VX_NIB_INV, -8.f * sx), res);
         }
         return res;
     } else if constexpr (QT == VX_Q8_0) {
@@ -186,16 +202,17 @@ __device__ __forceinline__ float vx_unit_dot_b1(const uint32_t (&r)[vx_unit<QT>:
         float slo = 0.f, shi = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const uint32_t lo = vx_and(r[4 + i], 0x0F0F0F0Fu);
-            const uint32_t hi = vx_and(r[4 + i], 0xF0F0F0F0u);
+            float wl[4], wh[4];
+            vx_nib4(r[4 + i], 0, wl);
+            vx_nib4(r[4 + i], 4, wh);
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                slo = __builtin_fmaf(vx_ub(lo, b), xv[4 * i + b], slo);
-                shi = __builtin_fmaf(vx_ub(hi, b), xv[32 + 4 * i + b], shi);
+                slo = __builtin_fmaf(wl[b], xv[4 * i + b], slo);
+                shi = __builtin_fmaf(wh[b], xv[32 + 4 * i + b], shi);
             }
         }
-        const float t0 = __builtin_fmaf(d * (float)sc0, slo, -(dmin * (float)m0) * sx0);
-        const float t1 = __builtin_fmaf(d * (float)sc1 * 0.0625f, shi, -(dmin * (float)m1) * sx1);
+        const float t0 = __builtin_fmaf(d * (float)sc0 * VX_NIB_INV, slo, -(dmin * (float)m0) * sx0);
+        const float t1 = __builtin_fmaf(d * (float)sc1 * VX_NIB_INV, shi, -(dmin * (float)m1) * sx1);
         return t0 + t1;
     }
 }

@@ -381,6 +381,37 @@ static int mfma_kernel(uint32_t qt, int ks, int pd) {
     return tab[q_index(qt)][pd == 4 ? 1 : 0][ks == 1 ? 0 : ks == 2 ? 1 : 2];
 }
 
+static int p1_kernel(uint32_t qt, int wgt) {
+    static const int tab[3][2] = {{K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q4_0_w512},
+                                  {K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q8_0_w512},
+                                  {K_vx_gemv_p1_q4_k_w1024, K_vx_gemv_p1_q4_k_w512}};
+    return tab[q_index(qt)][wgt == 1024 ? 0 : 1];
+}
+
+static int h16_kernel(uint32_t qt, int ks) {
+    static const int tab[3][3] = {
+        {K_vx_gemv_h16_q4_0_s1, K_vx_gemv_h16_q4_0_s2, K_vx_gemv_h16_q4_0_s4},
+        {K_vx_gemv_h16_q8_0_s1, K_vx_gemv_h16_q8_0_s2, K_vx_gemv_h16_q8_0_s4},
+        {K_vx_gemv_h16_q4_k_s1, K_vx_gemv_h16_q4_k_s2, K_vx_gemv_h16_q4_k_s4}};
+    return tab[q_index(qt)][ks == 1 ? 0 : ks == 2 ? 1 : 2];
+}
+
+// K-split of a matrix-core launch: the smallest of 1, 2, 4 whose grid of
+// 4 / ks row tiles per workgroup gives 1.3 workgroups per CU.
+static int pick_ksplit(vx_ctx ctx, uint32_t ntiles, const char* env) {
+    int ks = 4;
+    for (int c : {1, 2, 4})
+        if ((uint64_t)ntiles * c / 4u >= (uint64_t)ctx->num_cus * 13u / 10u) {
+            ks = c;
+            break;
+        }
+    if (const char* e = std::getenv(env)) {
+        const int v = std::atoi(e);
+        if (v == 1 || v == 2 || v == 4) ks = v;
+    }
+    return ks;
+}
+
 static int generic_kernel(uint32_t qt) {
     return qt == VX_Q4_0 ? K_vx_gemv_generic_q4_0 : qt == VX_Q8_0 ? K_vx_gemv_generic_q8_0 : K_vx_gemv_generic_q4_k;
 }
@@ -444,20 +475,33 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
     const char* bmode = std::getenv("VX_GEMV_BATCHED");
-    const bool use_mfma = fast && K % 256 == 0 && !(bmode && std::strcmp(bmode, "simt") == 0);
-    if (B >= 2 && use_mfma) {
+    const bool force_simt = bmode && std::strcmp(bmode, "simt") == 0;
+    const bool use_f32mfma = bmode && std::strcmp(bmode, "mfma32") == 0;
+    if (B >= 2 && fast && !force_simt && !use_f32mfma) {
+        // f16 matrix-core path (two f16 levels of x): up to 16 batch columns
+        // per launch, LDS = 512-k chunk of x levels + sums + exponents.
+        const uint32_t ntiles = (M + 15u) / 16u;
+        const int ks = pick_ksplit(ctx, ntiles, "VX_H16_KS");
+        const uint32_t tg_per_wg = 4u / (uint32_t)ks;
+        const uint32_t grid = (ntiles + tg_per_wg - 1) / tg_per_wg;
+        const size_t lds = (512u / 32u) * (2u * 64u * 16u + 16u * 4u) + 64u * 4u + 16u * 4u;
+        if (lds > budget) return fail(VX_ERR_UNSUPPORTED, "LDS budget too small");
+        for (uint32_t b0 = 0; b0 < B; b0 += 16) {
+            a.B = B - b0 < 16 ? B - b0 : 16;
+            a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
+            a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
+            a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
+            a.chunk_units = 512u / 64u;
+            a.upitch = 0;
+            s = launch(ctx, h16_kernel(w->qtype, ks), dim3(grid), dim3(VX_WG), lds, stream, a);
+            if (s) return s;
+        }
+        return VX_OK;
+    }
+    if (B >= 2 && fast && K % 256 == 0 && use_f32mfma) {
         // Matrix-core path: up to 16 batch columns per launch, f32 MFMA.
         const uint32_t ntiles = (M + 15u) / 16u;
-        int ks = 4;
-        for (int c : {1, 2, 4})
-            if ((uint64_t)ntiles * c / 4u >= (uint64_t)ctx->num_cus * 13u / 10u) {
-                ks = c;
-                break;
-            }
-        if (const char* e = std::getenv("VX_MFMA_KS")) {
-            const int v = std::atoi(e);
-            if (v == 1 || v == 2 || v == 4) ks = v;
-        }
+        const int ks = pick_ksplit(ctx, ntiles, "VX_MFMA_KS");
         int pd = 4;
         if (const char* e = std::getenv("VX_MFMA_PD")) pd = std::atoi(e) == 2 ? 2 : 4;
         // k per LDS chunk (16 columns x (kc + 4) floats): a multiple of 256 * ks
@@ -482,6 +526,10 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         }
         return VX_OK;
     }
+    // batch-1 kernel: the persistent one (default), or the per-row-group
+    // one with VX_GEMV_B1=rows (also used when x does not fit its LDS)
+    const char* b1env = std::getenv("VX_GEMV_B1");
+    const bool b1_rows = b1env && std::strcmp(b1env, "rows") == 0;
     uint32_t b0 = 0;
     while (b0 < B) {
         const uint32_t rem = B - b0;
@@ -508,6 +556,18 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             k = i8b1_kernel(w->qtype, R);
             rows_per_wg = 4u * R;
             lds = (size_t)a.upitch * 152u;
+        } else if (NB == 1 && a.nunits <= 256u && !b1_rows) {
+            // Persistent path: one workgroup per CU, all of x in LDS
+            // (16 slots x odd pitch x 16 B) plus the per-unit block sums.
+            int wgt = 1024;
+            if (const char* e = std::getenv("VX_P1_WG")) wgt = std::atoi(e) == 512 ? 512 : 1024;
+            a.chunk_units = a.nunits;
+            a.upitch = a.nunits | 1u;
+            lds = (size_t)16u * a.upitch * 16u + (size_t)a.nunits * 8u;
+            s = launch(ctx, p1_kernel(w->qtype, wgt), dim3((uint32_t)ctx->num_cus), dim3((uint32_t)wgt), lds, stream, a);
+            if (s) return s;
+            b0 += NB;
+            continue;
         } else if (NB == 1) {
             const int R = pick_rows_per_wave(ctx, w->qtype, M);
             // x chunk: up to 255 units (16 slots x odd pitch x 16 B <= 64 KB)
