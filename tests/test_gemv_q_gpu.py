@@ -142,6 +142,56 @@ def test_gemv_x_edge_values(qgemv, qtype):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("B", [2, 5, 8, 9])
+def test_gemv_batched_x_edge_values(qgemv, qtype, B):
+    """Batched (matrix-core) path: per column, blocks of x that are zero,
+    tiny, huge or hold one outlier. x is split per 32-block into two int8
+    levels there (error <= max|x_blk| / 64008 per element), so each column
+    is checked on its own at the spec tolerance and at 2e-4."""
+    M, K = 70, 4096
+    note(f"gemv batched edge x {QN[qtype]} B={B}")
+    w = S.quant_weights(qtype, M, K, seed=21, device=DEV)
+    x = S.activations(B, K, seed=22, device=DEV)
+    x[:, 0:32] = 0.0
+    x[1::2, 32:64] *= 1e-30
+    x[0::2, 64:96] *= 1e30
+    x[:, 96:128] *= 1e-3
+    x[:, 100] = 50.0
+    y = torch.full((B, M), float("nan"), device=DEV)
+    qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t())
+    torch.cuda.synchronize()
+    ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
+    got = y.cpu().numpy().T
+    for b in range(B):
+        assert_close(got[:, b], ref[:, b], what=f"column {b}")
+        assert_close(got[:, b], ref[:, b], tol=2e-4, what=f"column {b} (two-level bound)")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("path", ["simt", "rows"])
+def test_gemv_alternate_kernels(qgemv, qtype, path, monkeypatch):
+    """The exact-f32 batched kernels (VX_GEMV_BATCHED=simt) and the
+    per-row-group batch-1 kernel (VX_GEMV_B1=rows) stay selectable."""
+    M, K = 131, 4096
+    if path == "simt":
+        monkeypatch.setenv("VX_GEMV_BATCHED", "simt")
+        Bs = [2, 4, 8, 16]
+    else:
+        monkeypatch.setenv("VX_GEMV_B1", "rows")
+        Bs = [1]
+    w = S.quant_weights(qtype, M, K, seed=31, device=DEV)
+    wn = w.cpu().numpy()
+    for B in Bs:
+        note(f"gemv {path} {QN[qtype]} B={B}")
+        x = S.activations(B, K, seed=32 + B, device=DEV)
+        y = torch.full((B, M), float("nan"), device=DEV)
+        qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t())
+        torch.cuda.synchronize()
+        ref = O.gemv_q_f64(qtype, wn, M, K, x.cpu().numpy())
+        assert_close(y.cpu().numpy().T, ref, tol=1e-4, what=f"{path} B={B}")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 def test_gemv_generic_paths(qgemv, qtype):
     """Odd block counts, padded (unaligned) row strides and strided x / y
     take the byte-level fallback or the scalar x staging."""

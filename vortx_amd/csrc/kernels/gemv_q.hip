@@ -611,389 +611,310 @@ __device__ __forceinline__ void vx_gemv_bn(const vx_gemv_args& a) {
 }
 
 // ------------------------------------------------------------------------
-// Batched path on the matrix cores: v_mfma_f32_16x16x4f32 with
-//   A = 16 rows x 4 k of exactly decoded f32 weights (lane l: row l%16,
-//       k-slot l/16),
-//   B = 4 k x 16 batch columns of f32 x from LDS (lane l: k-slot l/16,
-//       column l%16; columns >= B read zeros),
-//   D = 16 rows x 16 columns in 4 VGPRs (lane l: rows 4(l/16)+v, column
-//       l%16),
-// so weights, x and the accumulation stay f32 and no per-block rescale is
-// needed. A wave owns 16-row tiles; within one MFMA the four k-slots take
-// element s of four consecutive units (64-weight groups) of the same rows, so
-// lane (r, q) streams unit 4g+q of row r with the same 128-bit loads as the
-// batch-1 kernel. KS waves of a workgroup split K (interleaved unit
-// groups) and their partial tiles are summed through LDS at the end; x is
-// staged per K chunk as [column][k] with a pitch of Kc + 4 floats (bank
-// conflict free for the 16 columns a 16-lane phase reads).
-template <int QT>
-__device__ __forceinline__ void vx_unit_decode64(const uint32_t (&r)[vx_unit<QT>::NW], uint32_t u, float (&w)[64]) {
+// Batched GEMV (2..8 columns per launch) on int8 matrix cores
+// (v_mfma_i32_16x16x64_i8).
+//   Per column and 32-block, x is split into two int8 levels,
+//     x ~= c2 (254 x1 + x2),  c2 = max|x_blk| / (126 * 254),
+//   so |x - that| <= c2 / 2 ~ 1.6e-5 max|x_blk|; the levels are staged in
+//   LDS as [column][unit][level][64 elements] with {c2, S = sum x} per
+//   block. Products and sums over a block are exact in int32.
+//   Rounds as in vx_gemv_p1's row tiles: a wave owns a 16-row tile, and in
+//   round q lane (row j = l%16, o = l/16) holds all of unit 4q + o of row j
+//   (loaded coalesced by lane 4j + o and moved with ds_bpermute).
+//   MFMA (s, cp) covers elements 16s..16s+15 of the four units for the
+//   column pair cp: k-group o of the B operand is lane (j, o)'s own piece s
+//   (exact int8), and A row 4o + 2c + L holds level L of column 2cp + c for
+//   unit 4q + o in k-group o only, so D row 4o + 2c + L lands in lane (j, o)
+//   (register 2c + L): the level sums of the lane's own unit. The lane then
+//   applies its block scales: acc += s_t c2 (254 D_L0 + D_L1) + s_o S per
+//   32-block (s_t = d, s_o = -8 d for Q4_0; d, 0 for Q8_0; d sc, -dmin m for
+//   Q4_K).
+// Work split: one workgroup of 1024 threads per CU (grid = CU count); CU c
+// owns row tiles c, c + G, ...; wave w takes rounds w, w + 16, ... of each
+// tile; the per-wave partial sums meet in LDS in a fixed order. The first
+// part of x is loaded before any weight (see vx_gemv_p1).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+#define VX_B_WG 1024
+#define VX_B_XPT 8  // float4 of x per thread loaded ahead of the weight stream
+
+// B operand for piece s (elements 16s..16s+15) of a unit held in r.
+template <int QT, int S>
+__device__ __forceinline__ i32x4 vx_m_piece(const uint32_t (&r)[vx_unit<QT>::NW]) {
+    i32x4 b;
     if constexpr (QT == VX_Q4_0) {
+        // block S/2: qs at byte 2 (block 0, dwords 0..4) or 20 (block 1,
+        // dwords 5..8); elements 0..15 low nibbles, 16..31 high nibbles.
+        constexpr int base = (S >> 1) ? 5 : 0;
+        constexpr uint32_t sh = ((S >> 1) ? 0u : 16u) + 4u * (S & 1);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
-            const float o = -8.f * d;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t qd = h ? r[5 + i] : __builtin_amdgcn_alignbit(r[i + 1], r[i], 16);
-                const uint32_t lo = vx_and(qd, 0x0F0F0F0Fu), hi = vx_and(qd >> 4, 0x0F0F0F0Fu);
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    w[32 * h + 4 * i + b] = __builtin_fmaf(vx_ub(lo, b), d, o);
-                    w[32 * h + 16 + 4 * i + b] = __builtin_fmaf(vx_ub(hi, b), d, o);
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t nx = (base + i + 1 <= 8) ? r[base + i + 1] : r[8];
+            b[i] = (int)(__builtin_amdgcn_alignbit(nx, r[base + i], sh) & 0x0F0F0F0Fu);
         }
     } else if constexpr (QT == VX_Q8_0) {
+        // block S/2 at byte 34 (S/2): elements 16(S&1).. at byte 2 + 16(S&1)
+        constexpr int base = (S >> 1) ? 9 + 4 * (S & 1) : 4 * (S & 1);
+        constexpr uint32_t sh = (S >> 1) ? 0u : 16u;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const float d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
-            const float o = -128.f * d;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t qd = h ? r[9 + i] : __builtin_amdgcn_alignbit(r[i + 1], r[i], 16);
-                const uint32_t uq = vx_xor(qd, 0x80808080u);  // q + 128, exact: (q+128) d - 128 d
-#pragma unroll
-                for (int b = 0; b < 4; ++b) w[32 * h + 4 * i + b] = __builtin_fmaf(vx_ub(uq, b), d, o);
-            }
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t nx = (base + i + 1 <= 16) ? r[base + i + 1] : r[16];
+            b[i] = (int)__builtin_amdgcn_alignbit(nx, r[base + i], sh);
         }
     } else {
-        float sc[4];
-        vx_unit_scales<QT>(r, u, sc);
+        // sub-block 2c + S/2: low (S/2 = 0) or high nibbles of qs bytes
+        // 16(S&1)..16(S&1)+15 of the quarter
+        constexpr int base = 4 + 4 * (S & 1);
+        constexpr uint32_t sh = 4u * (S >> 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t lo = vx_and(r[4 + i], 0x0F0F0F0Fu), hi = vx_and(r[4 + i] >> 4, 0x0F0F0F0Fu);
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                w[4 * i + b] = __builtin_fmaf(vx_ub(lo, b), sc[0], sc[1]);
-                w[32 + 4 * i + b] = __builtin_fmaf(vx_ub(hi, b), sc[2], sc[3]);
-            }
-        }
+        for (int i = 0; i < 4; ++i)
+            b[i] = (int)(__builtin_amdgcn_alignbit(r[base + i], r[base + i], sh) & 0x0F0F0F0Fu);
+    }
+    return b;
+}
+
+// Scale terms (s_t, s_o) of the two 32-blocks of a unit.
+template <int QT>
+__device__ __forceinline__ void vx_m_scales(const uint32_t (&r)[vx_unit<QT>::NW], uint32_t u, float (&st)[2],
+                                            float (&so)[2]) {
+    if constexpr (QT == VX_Q4_0) {
+        st[0] = vx_f16_to_f32(r[0]);
+        st[1] = vx_f16_to_f32(r[4] >> 16);
+        so[0] = -8.f * st[0];
+        so[1] = -8.f * st[1];
+    } else if constexpr (QT == VX_Q8_0) {
+        st[0] = vx_f16_to_f32(r[0]);
+        st[1] = vx_f16_to_f32(r[8] >> 16);
+        so[0] = 0.f;
+        so[1] = 0.f;
+    } else {
+        const float d = vx_f16_to_f32(r[0]);
+        const float dmin = vx_f16_to_f32(r[0] >> 16);
+        uint32_t sc0, m0, sc1, m1;
+        vx_q4k_scales(r[1], r[2], r[3], u & 3u, sc0, m0, sc1, m1);
+        st[0] = d * (float)sc0;
+        st[1] = d * (float)sc1;
+        so[0] = -(dmin * (float)m0);
+        so[1] = -(dmin * (float)m1);
     }
 }
 
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-// One 16-row tile per wave. The wave's unit groups (256 k each) are
-// g = ks, ks + KS, ...; their weights are loaded PD groups ahead in a
-// register ring, across LDS chunk boundaries, so HBM latency overlaps the
-// MFMA work. kc / 256 (groups per chunk) is a multiple of KS, so all waves
-// of a workgroup cross chunk boundaries - and reach the staging barriers -
-// at the same loop step.
-template <int QT, int KS, int PD>
-__device__ __forceinline__ void vx_gemv_mfma(const vx_gemv_args& a) {
+template <int QT, int NCP, bool XV>
+__device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
-    constexpr int TG = 4 / KS;  // tiles per workgroup
-    float* xs = (float*)vx_lds_x;
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t i16 = lane & 15u, q = lane >> 4;
-    const uint32_t ks = wave % KS;
-    const uint32_t tile = blockIdx.x * TG + wave / KS;
-    const uint32_t kc = a.chunk_units * 64u;  // k per LDS chunk, multiple of 256 * KS
-    const uint32_t pitch = kc + 4u;
-    const uint32_t ngroups = a.K / 256u;
-    const uint32_t nj = ngroups > ks ? (ngroups - ks + KS - 1) / KS : 0u;  // this wave's groups
-    const uint32_t row = min(tile * 16u + i16, a.M - 1u);  // rows past M read the last row
-    const uint8_t* wrow = a.w + (uint64_t)row * a.row_stride;
+    constexpr int NC = 2 * NCP;
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t j = lane & 15u, o = lane >> 4;
+    const uint32_t G = gridDim.x, cu = blockIdx.x;
+    const uint32_t B = a.B;
+    const uint32_t nunits = a.nunits;
+    const uint32_t ntiles = (a.M + 15u) >> 4;
+    const uint32_t nts = ntiles > cu ? (ntiles - cu + G - 1u) / G : 0u;
+    const uint32_t rpt = (nunits + 3u) >> 2;  // rounds per tile
+    const uint32_t upw = (rpt + 15u) >> 4;    // round slots per wave per tile
+    const uint32_t nitems = nts * upw;
 
-    f32x4v acc[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    // LDS: xq [col][unit][2][64] int8 | scl [col][unit] {c2_0, S_0, c2_1,
+    // S_1} | red [slot][16 waves][col][16] | 64 zero bytes at a.upitch.
+    uint8_t* xq = (uint8_t*)vx_lds_x;
+    f32x4* scl = (f32x4*)(xq + 128u * B * nunits);
+    float* red = (float*)(scl + B * nunits);
+    if (t < 16u) ((uint32_t*)(xq + a.upitch))[t] = 0u;
 
-    uint32_t wr[PD][NW];
+    // 1. x: float4 f = (column f / (16 nunits), unit, slot); the first
+    //    VX_B_XPT per thread are loaded before the issue-order barrier.
+    const uint32_t per_col = nunits * 16u, total = B * per_col;
+    auto xload = [&](uint32_t f) {
+        const uint32_t col = f / per_col, rem = f - col * per_col;
+        const int64_t k = 4 * (int64_t)rem;  // 64 u + 4 slot
+        if constexpr (XV) return *(const f32x4*)(a.x + (int64_t)col * a.xs_b + k);
+        const float* xp = a.x + (int64_t)col * a.xs_b + k * a.xs_k;
+        return f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+    };
+    f32x4 xr[VX_B_XPT];
 #pragma unroll
-    for (int p = 0; p < PD; ++p) {
-        const uint32_t g = ks + KS * min((uint32_t)p, nj ? nj - 1u : 0u);
-        vx_load_unit<QT>(wrow, 4u * min(g, ngroups - 1u) + q, wr[p]);
+    for (int i = 0; i < VX_B_XPT; ++i) {
+        if ((uint32_t)i * VX_B_WG >= total) break;  // uniform
+        xr[i] = xload(min(t + VX_B_WG * (uint32_t)i, total - 1u));
     }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
-    uint32_t cur_chunk = 0xFFFFFFFFu;
-    // every wave runs the same number of outer steps (the max over waves) so
-    // the staging barriers line up; steps past a wave's last group skip work.
-    const uint32_t nj_max = (ngroups + KS - 1) / KS;
-    for (uint32_t j0 = 0; j0 < nj_max; j0 += PD) {
+    const uint32_t lrow = lane >> 2, lu = lane & 3u;
+    const uint32_t perm = 4u * (4u * j + o);
+    auto rowbase = [&](uint32_t ts) {
+        const uint32_t row = min((cu + ts * G) * 16u + lrow, a.M - 1u);
+        return a.w + (uint64_t)row * a.row_stride;
+    };
+    auto unit_of = [&](uint32_t k) { return min(4u * (wave + 16u * k) + lu, nunits - 1u); };
+    uint32_t pts = 0, pk = 0;
+    const uint8_t* prow = rowbase(0u);
+    auto padv = [&]() {
+        if (++pk == upw) {
+            pk = 0;
+            if (pts + 1u < nts) {
+                ++pts;
+                prow = rowbase(pts);
+            } else {
+                pk = upw - 1u;  // past the end: repeat the last item
+            }
+        }
+    };
+    uint32_t wr[2][NW];
+    vx_load_unit<QT>(prow, unit_of(0u), wr[0]);
+    padv();
+
+    // 2. split x into two int8 levels per 32-block (8 float4 = 8 lanes).
+    auto split = [&](uint32_t f, f32x4 v, bool in) {
+        if (!in) v = f32x4{0.f, 0.f, 0.f, 0.f};
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        float ps = (v.x + v.y) + (v.z + v.w);
 #pragma unroll
-        for (int p = 0; p < PD; ++p) {
-            const uint32_t j = j0 + p;
-            if (j >= nj_max) break;  // uniform across the workgroup
-            const uint32_t g = ks + KS * j;
-            const uint32_t chunk = (KS * j * 256u) / kc;  // same for every ks
-            if (chunk != cur_chunk) {
-                cur_chunk = chunk;
-                const uint32_t k0 = chunk * kc;
-                const uint32_t klen = min(kc, a.K - k0);
-                __syncthreads();
-                for (uint32_t f = threadIdx.x; f < 16u * (kc / 4u); f += VX_WG) {
-                    const uint32_t b = f / (kc / 4u), k4 = 4u * (f % (kc / 4u));
-                    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-                    if (b < a.B && k4 < klen) {
-                        const int64_t k = (int64_t)k0 + k4;
-                        if (a.x_vec) {
-                            v = *(const f32x4*)(a.x + b * a.xs_b + k);
-                        } else {
-                            const float* xp = a.x + b * a.xs_b + k * a.xs_k;
-                            v = f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+        for (int sft = 1; sft < 8; sft <<= 1) {
+            m = fmaxf(m, __shfl_xor(m, sft, 64));
+            ps += __shfl_xor(ps, sft, 64);
+        }
+        const bool fin = m < __builtin_inff();
+        const float c1 = m * (1.f / 126.f), c2 = c1 * (1.f / 254.f);
+        const float i1 = (fin && m > 0.f) ? 126.f / m : 0.f, i2 = i1 * 254.f;
+        uint32_t pk0 = 0, pk1 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float q1 = __builtin_rintf(v[e] * i1);
+            const float r1 = __builtin_fmaf(-q1, c1, v[e]);
+            const float q2 = __builtin_rintf(r1 * i2);
+            pk0 |= ((uint32_t)(int)q1 & 0xFFu) << (8 * e);
+            pk1 |= ((uint32_t)(int)q2 & 0xFFu) << (8 * e);
+        }
+        if (in) {
+            const uint32_t cu_ = f >> 4, w4 = f & 15u;  // cu_ = column * nunits + unit
+            uint32_t* xu = (uint32_t*)(xq + 128u * cu_) + w4;
+            xu[0] = pk0;
+            xu[16] = pk1;
+            if ((f & 7u) == 0u) {
+                float* sc = (float*)(scl + cu_) + 2u * (w4 >> 3);
+                sc[0] = fin ? c2 : m;  // non-finite x: propagate into y
+                sc[1] = ps;
+            }
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < VX_B_XPT; ++i) {
+        if ((uint32_t)i * VX_B_WG >= total) break;
+        const uint32_t f = t + VX_B_WG * (uint32_t)i;
+        split(f, xr[i], f < total);
+    }
+    for (uint32_t f0 = VX_B_XPT * VX_B_WG; f0 < total; f0 += VX_B_WG) {
+        const uint32_t f = f0 + t;
+        split(f, xload(min(f, total - 1u)), f < total);
+    }
+    __syncthreads();
+
+    // 3. rounds (ring of two).
+    vx_load_unit<QT>(prow, unit_of(pk), wr[1]);
+    padv();
+    const uint32_t ai = lane & 15u, ao = lane >> 4;
+    const bool a_on = (ai >> 2) == ao;
+    const uint32_t ac = (ai >> 1) & 1u, aL = ai & 1u;
+    const bool ragged = (nunits & 3u) != 0u;
+    float acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    uint32_t ts = 0, k = 0;
+    auto body = [&](uint32_t (&rl)[NW]) {
+        const uint32_t q = wave + 16u * k;  // round of this tile
+        if (q < rpt) {
+            uint32_t r[NW];
+#pragma unroll
+            for (int i = 0; i < NW; ++i) r[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)perm, (int)rl[i]);
+            const uint32_t u = min(4u * q + o, nunits - 1u);
+            const uint32_t ua = min(4u * q + ao, nunits - 1u);
+            uint32_t abase[NCP];
+#pragma unroll
+            for (int cp = 0; cp < NCP; ++cp) {
+                const uint32_t col = 2u * cp + ac;
+                abase[cp] = (a_on && col < B) ? (128u * (col * nunits + ua) + 64u * aL) : a.upitch;
+            }
+            // Pieces 2b and 2b + 1 share block b's scales: the second MFMA
+            // accumulates onto the first. Then per column c of the pair
+            // T = 254 D_L0 + D_L1 (|D| < 2^20: exact in int32).
+            const i32x4 z = i32x4{0, 0, 0, 0};
+            float tq[NCP][2][2];
+#pragma unroll
+            for (int bb = 0; bb < 2; ++bb) {
+                const i32x4 bw0 = bb ? vx_m_piece<QT, 2>(r) : vx_m_piece<QT, 0>(r);
+                const i32x4 bw1 = bb ? vx_m_piece<QT, 3>(r) : vx_m_piece<QT, 1>(r);
+#pragma unroll
+                for (int cp = 0; cp < NCP; ++cp) {
+                    // only the 16 lanes of k-group rows read LDS; the rest are zero
+                    i32x4 a0 = z, a1 = z;
+                    if (a_on && abase[cp] != a.upitch) {
+                        const uint8_t* ap = xq + abase[cp] + 32u * bb;
+                        a0 = *(const i32x4*)ap;
+                        a1 = *(const i32x4*)(ap + 16u);
+                    }
+                    i32x4 dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bw0, z, 0, 0, 0);
+                    dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bw1, dd, 0, 0, 0);
+                    tq[cp][0][bb] = (float)(254 * dd[0] + dd[1]);
+                    tq[cp][1][bb] = (float)(254 * dd[2] + dd[3]);
+                }
+            }
+            float st[2], so[2];
+            vx_m_scales<QT>(r, u, st, so);
+            if (!(ragged && 4u * q + o >= nunits)) {
+#pragma unroll
+                for (int cp = 0; cp < NCP; ++cp)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) {
+                        const uint32_t col = 2u * cp + c;
+                        if (col < B) {
+                            const f32x4 sc = scl[col * nunits + u];
+                            float v = acc[2 * cp + c];
+                            v = __builtin_fmaf(st[0], sc.x * tq[cp][c][0], v);
+                            v = __builtin_fmaf(st[1], sc.z * tq[cp][c][1], v);
+                            if constexpr (QT != VX_Q8_0) {
+                                v = __builtin_fmaf(so[0], sc.y, v);
+                                v = __builtin_fmaf(so[1], sc.w, v);
+                            }
+                            acc[2 * cp + c] = v;
                         }
                     }
-                    *(f32x4*)(xs + b * pitch + k4) = v;
-                }
-                __syncthreads();
-            }
-            if (j < nj) {
-                float w[64];
-                vx_unit_decode64<QT>(wr[p], 4u * g + q, w);
-                // prefetch the group PD steps ahead into the freed slot
-                const uint32_t jn = min(j + PD, nj - 1u);
-                vx_load_unit<QT>(wrow, 4u * (ks + KS * jn) + q, wr[p]);
-                const float* xb = xs + i16 * pitch + (g * 256u - chunk * kc) + 64u * q;
-#pragma unroll
-                for (int s4 = 0; s4 < 16; ++s4) {
-                    const f32x4 xv = *(const f32x4*)(xb + 4 * s4);
-                    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 0], xv.x, acc[0], 0, 0, 0);
-                    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 1], xv.y, acc[1], 0, 0, 0);
-                    acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 2], xv.z, acc[2], 0, 0, 0);
-                    acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[4 * s4 + 3], xv.w, acc[3], 0, 0, 0);
-                }
             }
         }
-    }
-
-    // Sum the accumulators, then the KS partial tiles through LDS; store
-    // rows 4(l/16)+v, column l%16.
-    f32x4v tot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    if constexpr (KS > 1) {
-        __syncthreads();
-        f32x4v* red = (f32x4v*)vx_lds_x;  // [wave][lane]
-        red[wave * 64 + lane] = tot;
-        __syncthreads();
-        if (ks == 0) {
+        vx_load_unit<QT>(prow, unit_of(pk), rl);
+        padv();
+        if (++k == upw) {
+            // row j's sums over the four units of this wave's rounds
 #pragma unroll
-            for (int o = 1; o < KS; ++o) tot += red[(wave + o) * 64 + lane];
-        }
-    }
-    if (ks == 0 && i16 < a.B) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint32_t r = tile * 16u + 4u * q + v;
-            if (r < a.M) a.y[(int64_t)r * a.ys_m + (int64_t)i16 * a.ys_b] = tot[v];
-        }
-    }
-}
-
-// ------------------------------------------------------------------------
-// Batched path on f16 matrix cores at f32 accuracy (B >= 2, 16 columns per
-// launch).
-//   D[i][j] = sum_k X[i][k] Wq[k][j] with v_mfma_f32_16x16x32_f16:
-//     Wq (B operand) = the block integers of 16 rows j (q - 8 for Q4_0, q
-//       for Q8_0 and Q4_K), exact in f16: nibbles / bytes are placed in the
-//       mantissa of 1024.0 and the offset is removed with an exact packed
-//       f16 subtraction;
-//     X (A operand) = 16 batch columns i of x in two f16 levels x1 + x2.
-//       Per chunk of 512 k and column, x is first scaled by 2^n so that the
-//       chunk's max |x| lies in [2^14, 2^15): then |x s - x1 - x2| <=
-//       max(2^-22 |x s|, 2^-25), i.e. finer than f32 rounding relative to
-//       the column's scale, with no f16 overflow or loss to subnormals;
-//   each level is one MFMA into the block's accumulator, and the lane that
-//   loaded row j applies the block scale: acc += d D (Q4_K: + (-dmin m) S,
-//   S the scaled block sum of x). At the end of a chunk acc_chunk * 2^-n is
-//   added to the running sum.
-// Lane l: row j = l%16 of the tile, k-octet o = l/16 of every 32-block
-//   (A and B operands), outputs D[4o+v][j] = y[row j][column 4o+v].
-// The four lanes of a row load the same 64-weight unit (the TA merges the
-// identical addresses) and each takes one octet of every block. Within an
-// octet, k follows the order in which the packing yields the pairs:
-//   (e0,e2) (e1,e3) (e4,e6) (e5,e7) of the octet's 8 elements, where
-//   Q4_0's octet o is elements 4o..4o+3 and 16+4o..16+4o+3 of its block
-//   (low and high nibbles of qs dword o), and Q8_0 / Q4_K's octet is
-//   elements 8o..8o+7.
-// LDS: per 32-block, level and octet, 16 columns x 16 bytes (lane l reads
-//   group (o, l%16): conflict free); then the Q4_K block sums [blk][col],
-//   the per-wave column maxima and the chunk exponents.
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4h __attribute__((ext_vector_type(4)));
-
-#define VX_H_KC 512u  // k per staged chunk
-#define VX_H_NG (VX_H_KC / 128u)  // 8-element groups per thread per chunk
-
-// Exact packed f16 subtraction of a small-integer offset from 1024 + q pairs.
-__device__ __forceinline__ uint32_t vx_h2_sub(uint32_t bits, float off) {
-    const _Float16 o = (_Float16)off;
-    const f16x2 v = __builtin_bit_cast(f16x2, bits) - f16x2{o, o};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-// f16 pairs (1024 + nibble) of the nibbles at bits (sh, sh + 16) of w.
-__device__ __forceinline__ uint32_t vx_nib_pair(uint32_t w, uint32_t sh) {
-    return ((w >> sh) & 0x000F000Fu) | 0x64006400u;
-}
-
-// x of one 8-element group (block blk, octet o, column col) of the chunk at
-// k0, in packing order. Q4_0 groups are two float4 at 4o and 16 + 4o, the
-// others at 8o and 8o + 4.
-template <int QT, int XV>
-__device__ __forceinline__ void vx_h_load(const vx_gemv_args& a, uint32_t k0, uint32_t blk, uint32_t o,
-                                          uint32_t col, bool live, float (&e)[8]) {
-    const uint32_t ka = k0 + blk * 32u + (QT == VX_Q4_0 ? 4u * o : 8u * o);
-    const uint32_t kb = ka + (QT == VX_Q4_0 ? 16u : 4u);
-    if constexpr (XV) {
-        f32x4 u = f32x4{0.f, 0.f, 0.f, 0.f}, v = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            const float* xc = a.x + (int64_t)col * a.xs_b;
-            u = *(const f32x4*)(xc + ka);
-            v = *(const f32x4*)(xc + kb);
-        }
-        e[0] = u.x; e[1] = u.z; e[2] = u.y; e[3] = u.w;
-        e[4] = v.x; e[5] = v.z; e[6] = v.y; e[7] = v.w;
-    } else {
-        const uint32_t ord[4] = {0u, 2u, 1u, 3u};
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const uint32_t k = (t < 4 ? ka : kb) + ord[t & 3];
-            e[t] = live ? a.x[(int64_t)col * a.xs_b + (int64_t)k * a.xs_k] : 0.f;
-        }
-    }
-}
-
-template <int QT, int KS, int XV>
-__device__ __forceinline__ void vx_gemv_h16(const vx_gemv_args& a) {
-    constexpr int TG = 4 / KS;  // 16-row tiles per workgroup
-    constexpr uint32_t NBLK = VX_H_KC / 32u;
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const uint32_t j16 = lane & 15u, o = lane >> 4;
-    const uint32_t ks = wave % KS;
-    const uint32_t tile = blockIdx.x * TG + wave / KS;
-    const uint32_t row = min(tile * 16u + j16, a.M - 1u);
-    const uint8_t* wrow = a.w + (uint64_t)row * a.row_stride;
-
-    uint4* xg = (uint4*)vx_lds_x;                          // [blk][level][octet][col]
-    float* sums = (float*)(xg + NBLK * 2u * 64u);           // [blk][col] (Q4_K)
-    float* wmax = sums + NBLK * 16u;                        // [wave][col]
-    int* nexp = (int*)(wmax + 64);                          // [col]
-
-    f32x4h acc = f32x4h{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t k0 = 0; k0 < a.K; k0 += VX_H_KC) {
-        const uint32_t klen = min(VX_H_KC, a.K - k0);  // a multiple of 64
-        // ---- stage: load the chunk, per-column max |x|
-        const uint32_t col = t & 15u;
-        float e[VX_H_NG][8];
-        float mx = 0.f;
-#pragma unroll
-        for (uint32_t g = 0; g < VX_H_NG; ++g) {
-            const uint32_t f = t + g * VX_WG;
-            const uint32_t go = (f >> 4) & 3u, blk = f >> 6;
-            vx_h_load<QT, XV>(a, k0, blk, go, col, col < a.B && blk * 32u < klen, e[g]);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(e[g][i]));
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        if (lane < 16u) wmax[wave * 16u + lane] = mx;
-        __syncthreads();  // also: every wave is done with the previous chunk
-        const float m = fmaxf(fmaxf(wmax[col], wmax[16u + col]), fmaxf(wmax[32u + col], wmax[48u + col]));
-        const int n = (m < __builtin_inff()) ? 15 - __builtin_amdgcn_frexp_expf(m) : 0;
-        if (t < 16u) nexp[t] = n;
-#pragma unroll
-        for (uint32_t g = 0; g < VX_H_NG; ++g) {
-            const uint32_t f = t + g * VX_WG;
-            const uint32_t go = (f >> 4) & 3u, blk = f >> 6;
-            uint32_t l1[4], l2[4];
-            float part = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; i += 2) {
-                const float v0 = __builtin_amdgcn_ldexpf(e[g][i], n), v1 = __builtin_amdgcn_ldexpf(e[g][i + 1], n);
-                part += v0 + v1;
-                const _Float16 h0 = (_Float16)v0, h1 = (_Float16)v1;
-                const _Float16 r0 = (_Float16)(v0 - (float)h0), r1 = (_Float16)(v1 - (float)h1);
-                l1[i / 2] = __builtin_bit_cast(uint32_t, f16x2{h0, h1});
-                l2[i / 2] = __builtin_bit_cast(uint32_t, f16x2{r0, r1});
+            for (int c = 0; c < NC; ++c) {
+                float v = acc[c] + __shfl_xor(acc[c], 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if ((uint32_t)c < B && lane < 16u) red[((ts * 16u + wave) * B + c) * 16u + lane] = v;
+                acc[c] = 0.f;
             }
-            const uint32_t base = blk * 128u + go * 16u + col;
-            xg[base] = uint4{l1[0], l1[1], l1[2], l1[3]};
-            xg[base + 64u] = uint4{l2[0], l2[1], l2[2], l2[3]};
-            if constexpr (QT == VX_Q4_K) {
-                part += __shfl_xor(part, 16, 64);
-                part += __shfl_xor(part, 32, 64);
-                if (go == 0u) sums[blk * 16u + col] = part;
-            }
+            k = 0;
+            ++ts;
         }
-        __syncthreads();
+    };
+    const uint32_t nfull = nitems & ~1u;
+    for (uint32_t it0 = 0; it0 < nfull; it0 += 2) {
+        body(wr[0]);
+        body(wr[1]);
+    }
+    if (nfull < nitems) body(wr[0]);
 
-        // ---- compute: units of this wave's k-slice, two 32-blocks each
-        f32x4h accc = f32x4h{0.f, 0.f, 0.f, 0.f};
-        const uint32_t u0 = k0 / 64u, un = klen / 64u;
-        for (uint32_t ul = ks; ul < un; ul += KS) {
-            uint32_t r[vx_unit<QT>::NW];
-            vx_load_unit<QT>(wrow, u0 + ul, r);
-            float sc[4];
-            if constexpr (QT == VX_Q4_K) vx_unit_scales<QT>(r, u0 + ul, sc);
+    // 4. per tile, row and column: sum the 16 waves in a fixed order.
+    __syncthreads();
+    for (uint32_t idx = t; idx < nts * 16u * B; idx += VX_B_WG) {
+        const uint32_t ts2 = idx / (16u * B), rem = idx - ts2 * 16u * B;
+        const uint32_t col = rem >> 4, jj = rem & 15u;
+        const uint32_t row = (cu + ts2 * G) * 16u + jj;
+        float sum = 0.f;
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t blk = 2u * ul + h;
-                uint32_t p[4];
-                float d;
-                if constexpr (QT == VX_Q4_0) {
-                    const uint32_t qd = h ? r[5 + o] : __builtin_amdgcn_alignbit(r[o + 1], r[o], 16);
-                    p[0] = vx_h2_sub(vx_nib_pair(qd, 0), 1032.f);
-                    p[1] = vx_h2_sub(vx_nib_pair(qd, 8), 1032.f);
-                    p[2] = vx_h2_sub(vx_nib_pair(qd, 4), 1032.f);
-                    p[3] = vx_h2_sub(vx_nib_pair(qd, 12), 1032.f);
-                    d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
-                } else if constexpr (QT == VX_Q8_0) {
-#pragma unroll
-                    for (int q = 0; q < 2; ++q) {
-                        const int di = 2 * (int)o + q;
-                        const uint32_t qd = h ? r[9 + di] : __builtin_amdgcn_alignbit(r[di + 1], r[di], 16);
-                        const uint32_t u = vx_xor(qd, 0x80808080u);  // q + 128
-                        p[2 * q] = vx_h2_sub((u & 0x00FF00FFu) | 0x64006400u, 1152.f);
-                        p[2 * q + 1] = vx_h2_sub(((u >> 8) & 0x00FF00FFu) | 0x64006400u, 1152.f);
-                    }
-                    d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
-                } else {
-                    const uint32_t w0 = r[4 + 2 * o], w1 = r[5 + 2 * o], sh = 4u * h;
-                    p[0] = vx_h2_sub(vx_nib_pair(w0, sh), 1024.f);
-                    p[1] = vx_h2_sub(vx_nib_pair(w0, sh + 8u), 1024.f);
-                    p[2] = vx_h2_sub(vx_nib_pair(w1, sh), 1024.f);
-                    p[3] = vx_h2_sub(vx_nib_pair(w1, sh + 8u), 1024.f);
-                    d = sc[2 * h];
-                }
-                const f16x8 bw = __builtin_bit_cast(f16x8, uint4{p[0], p[1], p[2], p[3]});
-                const uint32_t gb = blk * 128u + o * 16u + j16;
-                const f16x8 x1 = __builtin_bit_cast(f16x8, xg[gb]);
-                const f16x8 x2 = __builtin_bit_cast(f16x8, xg[gb + 64u]);
-                f32x4h dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, bw, f32x4h{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(x2, bw, dd, 0, 0, 0);
-                if constexpr (QT == VX_Q4_K) {
-                    const f32x4 sv = *(const f32x4*)(sums + blk * 16u + 4u * o);
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) accc[v] = __builtin_fmaf(sc[2 * h + 1], sv[v], accc[v]);
-                }
-#pragma unroll
-                for (int v = 0; v < 4; ++v) accc[v] = __builtin_fmaf(d, dd[v], accc[v]);
-            }
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] += __builtin_amdgcn_ldexpf(accc[v], -nexp[4u * o + v]);
-    }
-    if constexpr (KS > 1) {
-        __syncthreads();
-        f32x4h* red = (f32x4h*)vx_lds_x;
-        red[wave * 64 + lane] = acc;
-        __syncthreads();
-        if (ks == 0) {
-#pragma unroll
-            for (int w = 1; w < KS; ++w) acc += red[(wave + w) * 64 + lane];
-        }
-    }
-    if (ks == 0) {
-        const uint32_t r0 = tile * 16u + j16;
-        if (r0 < a.M) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t c = 4u * o + v;
-                if (c < a.B) a.y[(int64_t)r0 * a.ys_m + (int64_t)c * a.ys_b] = acc[v];
-            }
-        }
+        for (int w = 0; w < 16; ++w) sum += red[((ts2 * 16u + w) * B + col) * 16u + jj];
+        if (row < a.M) a.y[(int64_t)row * a.ys_m + (int64_t)col * a.ys_b] = sum;
     }
 }
 
@@ -1050,17 +971,13 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
         if (a.x_vec) vx_gemv_bn<QT, NB, R, LPR, true>(a);                                         \
         else vx_gemv_bn<QT, NB, R, LPR, false>(a);                                                \
     }
-#define VX_GEMV_MFMA(QT, QN, KS, PD)                                                              \
-    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_mfma_##QN##_s##KS##_p##PD(vx_gemv_args a) { \
-        vx_gemv_mfma<QT, KS, PD>(a);                                                              \
-    }
-#define VX_GEMV_H16(QT, QN, KS)                                                                 \
-    extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_h16_##QN##_s##KS(vx_gemv_args a) {  \
-        if (a.x_vec) vx_gemv_h16<QT, KS, 1>(a); else vx_gemv_h16<QT, KS, 0>(a);                \
-    }
 #define VX_GEMV_P1(QT, QN, P, WGT)                                                              \
     extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(vx_gemv_args a) {  \
         if (a.x_vec) vx_gemv_p1<QT, P, WGT, true>(a); else vx_gemv_p1<QT, P, WGT, false>(a);   \
+    }
+#define VX_GEMV_I8B(QT, QN, NCP)                                                                \
+    extern "C" __global__ __launch_bounds__(VX_B_WG) void vx_gemv_i8b_##QN##_c##NCP(vx_gemv_args a) { \
+        if (a.x_vec) vx_gemv_i8b<QT, NCP, true>(a); else vx_gemv_i8b<QT, NCP, false>(a);        \
     }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
@@ -1075,15 +992,6 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     VX_GEMV_BN(QT, QN, 4, 2, 64)                                                                    \
     VX_GEMV_BN(QT, QN, 8, 2, 32)                                                                    \
     VX_GEMV_BN(QT, QN, 16, 2, 16)                                                                   \
-    VX_GEMV_H16(QT, QN, 1)                                                                         \
-    VX_GEMV_H16(QT, QN, 2)                                                                         \
-    VX_GEMV_H16(QT, QN, 4)                                                                         \
-    VX_GEMV_MFMA(QT, QN, 1, 2)                                                                      \
-    VX_GEMV_MFMA(QT, QN, 2, 2)                                                                      \
-    VX_GEMV_MFMA(QT, QN, 4, 2)                                                                      \
-    VX_GEMV_MFMA(QT, QN, 1, 4)                                                                      \
-    VX_GEMV_MFMA(QT, QN, 2, 4)                                                                      \
-    VX_GEMV_MFMA(QT, QN, 4, 4)                                                                      \
     extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_generic_##QN(vx_gemv_args a) {     \
         vx_gemv_generic<QT>(a);                                                                     \
     }                                                                                               \
@@ -1098,3 +1006,12 @@ VX_GEMV_P1(VX_Q4_K, q4_k, 2, 1024)
 VX_GEMV_P1(VX_Q4_0, q4_0, 4, 512)
 VX_GEMV_P1(VX_Q8_0, q8_0, 3, 512)
 VX_GEMV_P1(VX_Q4_K, q4_k, 4, 512)
+VX_GEMV_I8B(VX_Q4_0, q4_0, 1)
+VX_GEMV_I8B(VX_Q4_0, q4_0, 2)
+VX_GEMV_I8B(VX_Q4_0, q4_0, 4)
+VX_GEMV_I8B(VX_Q8_0, q8_0, 1)
+VX_GEMV_I8B(VX_Q8_0, q8_0, 2)
+VX_GEMV_I8B(VX_Q8_0, q8_0, 4)
+VX_GEMV_I8B(VX_Q4_K, q4_k, 1)
+VX_GEMV_I8B(VX_Q4_K, q4_k, 2)
+VX_GEMV_I8B(VX_Q4_K, q4_k, 4)

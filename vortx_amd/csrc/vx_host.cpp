@@ -370,17 +370,6 @@ static int bn_kernel(uint32_t qt, int NB) {
     return tab[q_index(qt)][ni];
 }
 
-static int mfma_kernel(uint32_t qt, int ks, int pd) {
-    static const int tab[3][2][3] = {
-        {{K_vx_gemv_mfma_q4_0_s1_p2, K_vx_gemv_mfma_q4_0_s2_p2, K_vx_gemv_mfma_q4_0_s4_p2},
-         {K_vx_gemv_mfma_q4_0_s1_p4, K_vx_gemv_mfma_q4_0_s2_p4, K_vx_gemv_mfma_q4_0_s4_p4}},
-        {{K_vx_gemv_mfma_q8_0_s1_p2, K_vx_gemv_mfma_q8_0_s2_p2, K_vx_gemv_mfma_q8_0_s4_p2},
-         {K_vx_gemv_mfma_q8_0_s1_p4, K_vx_gemv_mfma_q8_0_s2_p4, K_vx_gemv_mfma_q8_0_s4_p4}},
-        {{K_vx_gemv_mfma_q4_k_s1_p2, K_vx_gemv_mfma_q4_k_s2_p2, K_vx_gemv_mfma_q4_k_s4_p2},
-         {K_vx_gemv_mfma_q4_k_s1_p4, K_vx_gemv_mfma_q4_k_s2_p4, K_vx_gemv_mfma_q4_k_s4_p4}}};
-    return tab[q_index(qt)][pd == 4 ? 1 : 0][ks == 1 ? 0 : ks == 2 ? 1 : 2];
-}
-
 static int p1_kernel(uint32_t qt, int wgt) {
     static const int tab[3][2] = {{K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q4_0_w512},
                                   {K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q8_0_w512},
@@ -388,28 +377,20 @@ static int p1_kernel(uint32_t qt, int wgt) {
     return tab[q_index(qt)][wgt == 1024 ? 0 : 1];
 }
 
-static int h16_kernel(uint32_t qt, int ks) {
+static int i8b_kernel(uint32_t qt, uint32_t B) {
     static const int tab[3][3] = {
-        {K_vx_gemv_h16_q4_0_s1, K_vx_gemv_h16_q4_0_s2, K_vx_gemv_h16_q4_0_s4},
-        {K_vx_gemv_h16_q8_0_s1, K_vx_gemv_h16_q8_0_s2, K_vx_gemv_h16_q8_0_s4},
-        {K_vx_gemv_h16_q4_k_s1, K_vx_gemv_h16_q4_k_s2, K_vx_gemv_h16_q4_k_s4}};
-    return tab[q_index(qt)][ks == 1 ? 0 : ks == 2 ? 1 : 2];
+        {K_vx_gemv_i8b_q4_0_c1, K_vx_gemv_i8b_q4_0_c2, K_vx_gemv_i8b_q4_0_c4},
+        {K_vx_gemv_i8b_q8_0_c1, K_vx_gemv_i8b_q8_0_c2, K_vx_gemv_i8b_q8_0_c4},
+        {K_vx_gemv_i8b_q4_k_c1, K_vx_gemv_i8b_q4_k_c2, K_vx_gemv_i8b_q4_k_c4}};
+    return tab[q_index(qt)][B <= 2 ? 0 : B <= 4 ? 1 : 2];
 }
 
-// K-split of a matrix-core launch: the smallest of 1, 2, 4 whose grid of
-// 4 / ks row tiles per workgroup gives 1.3 workgroups per CU.
-static int pick_ksplit(vx_ctx ctx, uint32_t ntiles, const char* env) {
-    int ks = 4;
-    for (int c : {1, 2, 4})
-        if ((uint64_t)ntiles * c / 4u >= (uint64_t)ctx->num_cus * 13u / 10u) {
-            ks = c;
-            break;
-        }
-    if (const char* e = std::getenv(env)) {
-        const int v = std::atoi(e);
-        if (v == 1 || v == 2 || v == 4) ks = v;
-    }
-    return ks;
+// LDS bytes of the int8 matrix-core batched kernel for B columns: x levels
+// (128 B per unit and column), block scales (16 B per unit and column),
+// per-wave partial sums (1 KB per row tile of the CU and column), 64 zero
+// bytes.
+static size_t i8b_lds(uint32_t B, uint32_t nunits, uint32_t nts) {
+    return (size_t)144u * B * nunits + (size_t)1024u * B * nts + 64u;
 }
 
 static int generic_kernel(uint32_t qt) {
@@ -476,55 +457,27 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
     const char* bmode = std::getenv("VX_GEMV_BATCHED");
     const bool force_simt = bmode && std::strcmp(bmode, "simt") == 0;
-    const bool use_f32mfma = bmode && std::strcmp(bmode, "mfma32") == 0;
-    if (B >= 2 && fast && !force_simt && !use_f32mfma) {
-        // f16 matrix-core path (two f16 levels of x): up to 16 batch columns
-        // per launch, LDS = 512-k chunk of x levels + sums + exponents.
-        const uint32_t ntiles = (M + 15u) / 16u;
-        const int ks = pick_ksplit(ctx, ntiles, "VX_H16_KS");
-        const uint32_t tg_per_wg = 4u / (uint32_t)ks;
-        const uint32_t grid = (ntiles + tg_per_wg - 1) / tg_per_wg;
-        const size_t lds = (512u / 32u) * (2u * 64u * 16u + 16u * 4u) + 64u * 4u + 16u * 4u;
-        if (lds > budget) return fail(VX_ERR_UNSUPPORTED, "LDS budget too small");
-        for (uint32_t b0 = 0; b0 < B; b0 += 16) {
-            a.B = B - b0 < 16 ? B - b0 : 16;
-            a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
-            a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
-            a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
-            a.chunk_units = 512u / 64u;
-            a.upitch = 0;
-            s = launch(ctx, h16_kernel(w->qtype, ks), dim3(grid), dim3(VX_WG), lds, stream, a);
-            if (s) return s;
+    if (B >= 2 && fast && !force_simt) {
+        // int8 matrix-core path, one workgroup per CU, up to 8 columns per
+        // launch (fewer when x of that many columns does not fit LDS).
+        const uint32_t nts = ((M + 15u) / 16u + (uint32_t)ctx->num_cus - 1u) / (uint32_t)ctx->num_cus;
+        uint32_t cpl = 8u;
+        while (cpl > 1u && i8b_lds(cpl < B ? cpl : B, a.nunits, nts) > budget) cpl >>= 1;
+        if (cpl >= 2u || i8b_lds(1u, a.nunits, nts) <= budget) {
+            for (uint32_t b0 = 0; b0 < B; b0 += cpl) {
+                a.B = B - b0 < cpl ? B - b0 : cpl;
+                a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
+                a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
+                a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
+                a.chunk_units = a.nunits;
+                a.upitch = (uint32_t)(i8b_lds(a.B, a.nunits, nts) - 64u);  // zero area offset
+                size_t lds = i8b_lds(a.B, a.nunits, nts);
+                if (lds < 82u * 1024u) lds = budget < 82u * 1024u ? budget : 82u * 1024u;
+                s = launch(ctx, i8b_kernel(w->qtype, a.B), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
+                if (s) return s;
+            }
+            return VX_OK;
         }
-        return VX_OK;
-    }
-    if (B >= 2 && fast && K % 256 == 0 && use_f32mfma) {
-        // Matrix-core path: up to 16 batch columns per launch, f32 MFMA.
-        const uint32_t ntiles = (M + 15u) / 16u;
-        const int ks = pick_ksplit(ctx, ntiles, "VX_MFMA_KS");
-        int pd = 4;
-        if (const char* e = std::getenv("VX_MFMA_PD")) pd = std::atoi(e) == 2 ? 2 : 4;
-        // k per LDS chunk (16 columns x (kc + 4) floats): a multiple of 256 * ks
-        const uint32_t step = 256u * (uint32_t)ks;
-        uint32_t kc = 1024u > step ? 1024u : step;
-        if (const char* e = std::getenv("VX_MFMA_KC")) kc = ((uint32_t)std::atoi(e) / step) * step;
-        if (kc < step) kc = step;
-        while (kc > step && (size_t)16u * (kc + 4u) * 4u > budget) kc -= step;
-        if ((size_t)16u * (kc + 4u) * 4u > budget) return fail(VX_ERR_UNSUPPORTED, "LDS budget too small");
-        const uint32_t tg_per_wg = 4u / (uint32_t)ks;
-        const uint32_t grid = (ntiles + tg_per_wg - 1) / tg_per_wg;
-        const size_t lds = (size_t)16u * (kc + 4u) * 4u;
-        for (uint32_t b0 = 0; b0 < B; b0 += 16) {
-            a.B = B - b0 < 16 ? B - b0 : 16;
-            a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
-            a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
-            a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
-            a.chunk_units = kc / 64u;
-            a.upitch = 0;
-            s = launch(ctx, mfma_kernel(w->qtype, ks, pd), dim3(grid), dim3(VX_WG), lds, stream, a);
-            if (s) return s;
-        }
-        return VX_OK;
     }
     // batch-1 kernel: the persistent one (default), or the per-row-group
     // one with VX_GEMV_B1=rows (also used when x does not fit its LDS)
