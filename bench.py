@@ -6,9 +6,11 @@ W 11008 x 4096, batch 1, throughput in GB/s of algorithmic bytes
 next of >= 512 MB of distinct weight copies (so the 256 MB Infinity Cache
 cannot serve them), inputs resident in HBM before timing starts.
 
-Secondary lines in the same JSON object: Q8_0 GEMV 4096 x 4096 b=1 (GB/s)
-and the f32 GEMM 4096^3 (TFLOP/s), each with its roofline, plus CPU
-baselines from the oracle's OpenMP restatements on the host cores.
+Secondary lines in the same JSON object: the other BASELINE GEMV configs
+(Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 b=1, Q4_0 11008 x 4096
+b=8, Q4_K 14336 x 4096 b=16; GB/s of algorithmic bytes) and the f32 GEMM
+4096^3 (TFLOP/s), each with its roofline, plus CPU baselines from the
+oracle's OpenMP restatements on the host cores.
 
 Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
 (captured eager launches) between two synchronizations (wall clock).
@@ -64,6 +66,7 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     nbytes = M * S.row_bytes(qtype, K)
     ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
     log(f"[{label}] generating {ncopy} weight copies ({ncopy * nbytes / 2**20:.0f} MiB)")
+    log(f"[copies] {ncopy} x {nbytes}")
     distinct = [S.quant_weights(qtype, M, K, seed=100 + i, device=dev) for i in range(min(4, ncopy))]
     ws = [distinct[i % len(distinct)].clone() for i in range(ncopy)]
     del distinct
@@ -197,8 +200,20 @@ def main() -> int:
 
     q40 = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0")
     log(f"[q4_0] {q40}")
-    q80 = time_gemv(8, 4096, 4096, 1, args.steps, args.warmup, "q8_0")
-    log(f"[q8_0] {q80}")
+    # secondary GEMV configs: (qtype, M, K, B, label, workload, traffic profile)
+    SECONDARY = [
+        (8, 4096, 4096, 1, "q8_0", "Q8_0 GEMV 4096x4096 batch 1", "gemv_q8_0_4096x4096_b1"),
+        (12, 32000, 4096, 1, "q4_k", "Q4_K GEMV 32000x4096 batch 1", "gemv_q4_k_32000x4096_b1"),
+        (2, 11008, 4096, 8, "q4_0_b8", "Q4_0 GEMV 11008x4096 batch 8", "gemv_q4_0_11008x4096_b8"),
+        (8, 4096, 4096, 8, "q8_0_b8", "Q8_0 GEMV 4096x4096 batch 8", "gemv_q8_0_4096x4096_b8"),
+        (12, 14336, 4096, 16, "q4_k_b16", "Q4_K GEMV 14336x4096 batch 16", "gemv_q4_k_14336x4096_b16"),
+    ]
+    sec = []
+    for qt, M, K, B, label, workload, prof in SECONDARY:
+        steps = max(100, args.steps // (2 if B > 1 or M > 20000 else 1))
+        r = time_gemv(qt, M, K, B, steps, args.warmup, label)
+        log(f"[{label}] {r}")
+        sec.append((workload, prof, r))
     gsteps = max(5, min(50, args.steps // 40))
     gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm] {gemm}")
@@ -233,8 +248,9 @@ def main() -> int:
         "roofline": roof_hbm(q40, "gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
         "secondary": [
-            {"workload": "Q8_0 GEMV 4096x4096 batch 1", "value": q80["value"], "unit": "GB/s",
-             "ms_per_step": q80["ms_per_step"], "roofline": roof_hbm(q80, "gemv_q8_0_4096x4096_b1")},
+            {"workload": wl, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
+             "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
+        ] + [
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
              "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
