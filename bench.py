@@ -147,6 +147,34 @@ def time_gemm(M: int, N: int, K: int, steps: int, warmup: int):
             "ms_per_step": wall * 1e3 / steps}
 
 
+def time_contiguous(shape, steps: int, warmup: int):
+    """vortx's Contiguous op (src/linalg/contiguous.rs) on a transposed f32
+    view: bytes = 8 per element (read + write); 4 rotating 256 MB sources."""
+    import torch
+
+    import vortx_amd as vx
+
+    dev = torch.device("cuda:0")
+    srcs = [torch.randn(shape, device=dev).t() for _ in range(4)]
+    out = torch.empty(srcs[0].shape, device=dev)
+    c = vx.Contiguous(0)
+    for i in range(warmup):
+        c.launch(out, srcs[i % 4])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        c.launch(out, srcs[i % 4])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    nbytes = 8 * out.numel()
+    return {"value": nbytes * steps / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / steps,
+            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
+
+
 def cpu_baselines(threads: int):
     """Oracle OpenMP restatements on the host cores (bounded samples)."""
     import numpy as np
@@ -217,6 +245,8 @@ def main() -> int:
     gsteps = max(5, min(50, args.steps // 40))
     gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm] {gemm}")
+    cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
+    log(f"[contiguous] {cont}")
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     cpu = None if args.no_cpu else cpu_baselines(threads)
@@ -251,6 +281,9 @@ def main() -> int:
             {"workload": wl, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
              "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
         ] + [
+            {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
+             "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],
+             "roofline": roof_hbm(cont, "contiguous_t8192")},
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
              "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",

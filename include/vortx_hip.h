@@ -163,12 +163,14 @@ int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 
 /* vx_gemv_q with options; flags is a bitwise OR of vx_gemv_flags.
- * By default every launch multiplies the exactly decoded weights with f32 x
- * (f32 FMA accumulation). VX_GEMV_X_INT8 (batch-1 launches) instead splits
- * each 32-element block of x into two int8 levels with one f32 scale,
- * x ~= c (254 x1 + x2) with |error| <= c/2 ~ 1.6e-5 max|x_block|, reduces
- * each weight block exactly in int32 (v_dot4_i32_i8) and combines blocks in
- * f32. */
+ * Batch 1 (B == 1) multiplies the exactly decoded weights with f32 x (f32
+ * FMA accumulation) by default. Batches (B >= 2) run on the int8 matrix
+ * cores: each 32-element block of each column of x is split into two int8
+ * levels with one f32 scale, x ~= c (254 x1 + x2), |error| <= c/2 ~
+ * 1.6e-5 max|x_block|; products and block sums are exact in int32 and the
+ * scaling is f32. VX_GEMV_X_INT8 applies the same split to batch-1 launches
+ * (reduced with v_dot4_i32_i8). The environment variable
+ * VX_GEMV_BATCHED=simt selects exact-f32 batch kernels instead. */
 typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1 } vx_gemv_flags;
 int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_cview* x, uint32_t flags);
@@ -177,6 +179,21 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
  * exactly representable in f32). out is an [M, K] view, any strides. */
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out,
                   const vx_qweight* w);
+
+/* ---- strided -> contiguous copy (4-byte elements) --------------------
+ * Replaces Contiguous::launch (src/linalg/contiguous.rs:22-119; shader
+ * vortx-shaders/src/linalg/contiguous.rs:59-90): out[i] = src[it(n,c,h,w)]
+ * over the canonicalized src view, i the row-major index. out must have the
+ * same size array as src and a contiguous layout (VX_ERR_SHAPE otherwise,
+ * where the reference panics). dev_offset is the optional `offset` tensor:
+ * null reads src at its view offset (TensorRef::buffer); non-null reads the
+ * raw buffer at the device u32 *dev_offset, ignoring the view offset
+ * (TensorRef::raw_buffer), as the reference does. Elements are copied as
+ * bits (f32, i32, u32 alike); indices are 64-bit (the shader's u32 index
+ * wraps past 2^32 elements); views of 2^32 elements or more return
+ * VX_ERR_UNSUPPORTED. Asynchronous on `stream`. */
+int vx_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                  const vx_cview* src, const uint32_t* dev_offset);
 
 /* Block geometry of a vx_qtype: weights per block and bytes per block. */
 int vx_qtype_info(uint32_t qtype, uint32_t* block_weights,

@@ -57,6 +57,8 @@ def lib():
                                              C.c_uint32, C.c_int]
         L.orc_q4k_scale_min.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_uint8), C.POINTER(C.c_uint8)]
         L.orc_max_threads.restype = C.c_int
+        L.orc_contiguous_u32.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]
+        L.orc_contiguous_u32.restype = C.c_int
         for name in ("orc_dequant", "orc_gemv_q_f64", "orc_gemv_q_f32_omp", "orc_gemm_ref_f32",
                      "orc_gemm_f64", "orc_gemm_tiled_f32_omp", "orc_q4k_scale_min"):
             if name != "orc_q4k_scale_min":
@@ -177,3 +179,34 @@ def gemm_tiled_f32_omp(a: np.ndarray, b: np.ndarray, nthreads: int = 0) -> np.nd
 
 def max_threads() -> int:
     return lib().orc_max_threads()
+
+
+# ----------------------------------------------------------- contiguous
+def canonicalize(shape, stride):
+    """src/shapes.rs:145-155: prepend size-1 dims up to rank 4 (their strides
+    are those of a contiguous layout of the padded sizes)."""
+    shape, stride = list(shape), list(stride)
+    pad = 4 - len(shape)
+    size = [1] * pad + shape
+    st = [0] * 4
+    acc = 1
+    for k in range(3, -1, -1):
+        st[k] = acc
+        acc *= size[k]
+    st[pad:] = stride
+    return size, st
+
+
+def contiguous_u32(src_flat: np.ndarray, shape, stride, offset: int = 0) -> np.ndarray:
+    """vortx-shaders/src/linalg/contiguous.rs:70-90 over a 4-byte element
+    buffer (viewed as uint32): the row-major copy of the view (shape, stride)
+    starting at element `offset`."""
+    buf = np.ascontiguousarray(src_flat).view(np.uint32)
+    size, st = canonicalize(shape, stride)
+    size_a = np.array(size, dtype=np.uint32)
+    st_a = np.array(st, dtype=np.uint32)
+    n = int(np.prod(size, dtype=np.int64))
+    out = np.empty(max(n, 1), dtype=np.uint32)
+    rc = lib().orc_contiguous_u32(_ptr(out), _ptr(buf), _ptr(size_a), _ptr(st_a), offset)
+    assert rc == 0
+    return out[:n].reshape(shape) if len(shape) else out[:n]

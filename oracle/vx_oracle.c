@@ -7,6 +7,11 @@
  *
  * What it restates, and what pins each part (checks live in tests/):
  *
+ *  - orc_contiguous_u32: vortx's contiguous shader (vortx-shaders/src/
+ *    linalg/contiguous.rs:59-90): thread i writes dest[i] = src[offset +
+ *    it(n, c, h, w)] with (n, c, h, w) the row-major split of i over the
+ *    canonical sizes and it() in u32 arithmetic (shape.rs:46-48), as the
+ *    shader does. Pinned against numpy's as_strided copy.
  *  - orc_f16_to_f32: IEEE-754 binary16 -> binary32, from the format's
  *    definition. Pinned exhaustively (all 65536 bit patterns) against
  *    numpy's float16 conversion.
@@ -343,4 +348,25 @@ int orc_max_threads(void) {
 #else
     return 1;
 #endif
+}
+
+/* vortx-shaders/src/linalg/contiguous.rs:70-90 (contiguous_impl): size and
+ * stride are the canonical [n, c, h, w] Shape fields; offset is the extra
+ * element offset (0 for the plain `contiguous` entry point). u32 index
+ * arithmetic like the shader. */
+int orc_contiguous_u32(uint32_t* dest, const uint32_t* src, const uint32_t* size, const uint32_t* stride,
+                       uint32_t offset) {
+    const uint32_t len = size[0] * size[1] * size[2] * size[3];
+    const uint32_t h_stride = size[3];
+    const uint32_t c_stride = size[2] * size[3];
+    const uint32_t n_stride = size[1] * size[2] * size[3];
+    for (uint32_t t = 0; t < len; ++t) {
+        const uint32_t n = t / n_stride;
+        const uint32_t c = (t % n_stride) / c_stride;
+        const uint32_t h = (t % c_stride) / h_stride;
+        const uint32_t w = t % h_stride;
+        const uint32_t it = n * stride[0] + c * stride[1] + h * stride[2] + w * stride[3];
+        dest[t] = src[offset + it];
+    }
+    return 0;
 }

@@ -219,3 +219,26 @@ def test_gemv_oracle_vs_numpy(qtype):
     np.testing.assert_allclose(O.gemv_q_f64(qtype, w, M, K, x), ref, rtol=1e-12, atol=1e-12)
     got = O.gemv_q_f32_omp(qtype, w, M, K, x, 2)
     assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("shape,stride,offset", [
+    ((7,), (3,), 2),
+    ((5, 6), (1, 5), 0),            # transposed 6x5
+    ((4, 3, 5), (1, 0, 4), 1),      # a broadcast axis (stride 0)
+    ((2, 3, 4, 5), (70, 20, 5, 1), 0),
+    ((2, 3, 4, 5), (1, 2, 6, 24), 3),
+])
+def test_oracle_contiguous_matches_numpy(shape, stride, offset):
+    """orc_contiguous_u32 (contiguous.rs:70-90) vs numpy's as_strided copy."""
+    rng = np.random.default_rng(5)
+    span = offset + sum((s - 1) * st for s, st in zip(shape, stride)) + 1
+    buf = rng.standard_normal(span + 4).astype(np.float32)
+    ref = np.lib.stride_tricks.as_strided(buf[offset:], shape=shape, strides=[s * 4 for s in stride]).copy()
+    got = O.contiguous_u32(buf, shape, stride, offset).view(np.float32)
+    assert np.array_equal(got.reshape(shape), ref)
+
+
+def test_oracle_canonicalize_rule():
+    """src/shapes.rs:145-155: leading size-1 dims with contiguous strides."""
+    assert O.canonicalize((5, 6), (1, 5)) == ([1, 1, 5, 6], [30, 30, 1, 5])
+    assert O.canonicalize((2, 3, 4, 5), (9, 8, 7, 6)) == ([2, 3, 4, 5], [9, 8, 7, 6])

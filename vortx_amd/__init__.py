@@ -7,7 +7,9 @@ Python-side mirror of the reference interface for this path:
 * :class:`Gemm` — ``Gemm::dispatch`` / ``dispatch_naive`` / ``dispatch_tiled``
   (src/linalg/gemm.rs:47-305) on f32 views: out = lhs * rhs;
 * :class:`QuantGemv` — block-quantized GEMV y = W x (Q8_0, Q4_0, Q4_K) and
-  dequantize, which the reference does not have.
+  dequantize, which the reference does not have;
+* :class:`Contiguous` — ``Contiguous::launch`` (src/linalg/contiguous.rs:22-119),
+  the strided -> contiguous copy of 4-byte elements.
 
 A view is either a torch tensor on the GPU (its sizes, strides and storage
 offset become the layout) or a ``(buffer, TensorLayout)`` pair, exactly like
@@ -24,7 +26,7 @@ from . import _ffi
 from ._ffi import (NONE_STRIDE, ROUTE_EMPTY, ROUTE_GEMV, ROUTE_NAIVE, ROUTE_TILED, VX_Q4_0, VX_Q4_K, VX_Q8_0,
                    VortxError, check, lib)
 
-__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
+__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "Contiguous", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
            "ROUTE_NAIVE", "ROUTE_TILED", "ROUTE_GEMV", "ROUTE_EMPTY", "qtype_info", "lib"]
 
 # Load eagerly: a missing library must fail at import, not at first call.
@@ -103,16 +105,18 @@ class TensorLayout:
         return bool(lib().vx_layout_is_contiguous(C.byref(self._c())))
 
 
-def _view_of(v, mutable: bool):
-    """torch tensor or (buffer, TensorLayout) -> VxCView / VxMView."""
+def _view_of(v, mutable: bool, any4: bool = False):
+    """torch tensor or (buffer, TensorLayout) -> VxCView / VxMView.
+    any4: accept any 4-byte element type (bit copies), not only float32."""
     import torch
+    ok = (lambda t: t.element_size() == 4) if any4 else (lambda t: t.dtype == torch.float32)
     if isinstance(v, tuple):
         buf, layout = v
-        if not (isinstance(buf, torch.Tensor) and buf.dtype == torch.float32 and buf.is_cuda):
+        if not (isinstance(buf, torch.Tensor) and ok(buf) and buf.is_cuda):
             raise TypeError("view buffer must be a float32 tensor on the GPU")
         base = buf.data_ptr()
     else:
-        if not (isinstance(v, torch.Tensor) and v.dtype == torch.float32 and v.is_cuda):
+        if not (isinstance(v, torch.Tensor) and ok(v) and v.is_cuda):
             raise TypeError("views must be float32 tensors on the GPU")
         if v.dim() > 4:
             raise VortxError(_ffi.VX_ERR_UNSUPPORTED, "tensors of ranks > 4 not supported")
@@ -232,3 +236,22 @@ class QuantGemv(_Context):
     def dequantize(self, out, w: QWeight, stream=None) -> None:
         ov, wc = _view_of(out, True), w._c()
         check(lib().vx_dequantize(self._h, _stream(stream), C.byref(ov), C.byref(wc)))
+
+
+class Contiguous(_Context):
+    """vortx's Contiguous op (src/linalg/contiguous.rs:11-119): copy a
+    strided view of 4-byte elements into a contiguous output of the same
+    size. ``offset`` is the optional device u32 tensor of the reference's
+    ``launch``: when given, the source's raw buffer is read at that offset and
+    the view's own offset is ignored, as in the reference."""
+
+    def launch(self, out, tensor, offset=None, stream=None) -> None:
+        import torch
+        ov, tv = _view_of(out, True, any4=True), _view_of(tensor, False, any4=True)
+        off = None
+        if offset is not None:
+            if not (isinstance(offset, torch.Tensor) and offset.is_cuda and offset.element_size() == 4
+                    and offset.numel() >= 1):
+                raise TypeError("offset must be a 4-byte integer tensor on the GPU")
+            off = offset.data_ptr()
+        check(lib().vx_contiguous(self._h, _stream(stream), C.byref(ov), C.byref(tv), off))

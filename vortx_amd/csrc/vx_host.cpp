@@ -26,6 +26,8 @@ extern const unsigned char vx_co_gemm[];
 extern const unsigned char vx_co_gemm_end[];
 extern const unsigned char vx_co_gemv_q[];
 extern const unsigned char vx_co_gemv_q_end[];
+extern const unsigned char vx_co_copy[];
+extern const unsigned char vx_co_copy_end[];
 }
 
 namespace vx {
@@ -63,7 +65,9 @@ static const char* const kKernelNames[K_COUNT] = {
 #include "vx_kernel_list.inc"
 #undef K
 };
-static bool kernel_in_gemm_module(int k) { return k <= K_vx_gemv_f32; }
+// The embedded code objects; every kernel name is unique across them.
+static const unsigned char* const kModules[] = {vx_co_gemm, vx_co_gemv_q, vx_co_copy};
+constexpr int kNumModules = 3;
 
 }  // namespace vx
 
@@ -71,8 +75,7 @@ struct vx_context {
     int device = 0;
     int num_cus = 0;
     size_t lds_per_block = 65536;
-    hipModule_t mod_gemm = nullptr;
-    hipModule_t mod_gemv = nullptr;
+    hipModule_t mods[vx::kNumModules] = {};
     hipFunction_t fn[vx::K_COUNT] = {};
 };
 
@@ -137,21 +140,30 @@ static int init(int device, vx_ctx* out) {
     }
     ctx->num_cus = prop.multiProcessorCount;
     ctx->lds_per_block = prop.sharedMemPerBlock;
-    e = hipModuleLoadData(&ctx->mod_gemm, vx_co_gemm);
-    if (e == hipSuccess) e = hipModuleLoadData(&ctx->mod_gemv, vx_co_gemv_q);
-    if (e != hipSuccess) {
-        if (ctx->mod_gemm) (void)hipModuleUnload(ctx->mod_gemm);
-        t_hip = e;
-        t_msg = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
-        delete ctx;
-        return VX_ERR_NO_CODE_OBJECT;
+    auto unload = [&]() {
+        for (hipModule_t m : ctx->mods)
+            if (m) (void)hipModuleUnload(m);
+    };
+    for (int i = 0; i < kNumModules; ++i) {
+        e = hipModuleLoadData(&ctx->mods[i], kModules[i]);
+        if (e != hipSuccess) {
+            unload();
+            t_hip = e;
+            t_msg = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
+            delete ctx;
+            return VX_ERR_NO_CODE_OBJECT;
+        }
     }
     for (int k = 0; k < K_COUNT; ++k) {
-        hipModule_t m = kernel_in_gemm_module(k) ? ctx->mod_gemm : ctx->mod_gemv;
-        e = hipModuleGetFunction(&ctx->fn[k], m, kKernelNames[k]);
+        e = hipErrorNotFound;
+        for (int i = 0; i < kNumModules && e != hipSuccess; ++i) {
+            e = hipModuleGetFunction(&ctx->fn[k], ctx->mods[i], kKernelNames[k]);
+            // a miss in one module is expected; do not leave it as the
+            // runtime's last error for the caller's next HIP call
+            if (e != hipSuccess) (void)hipGetLastError();
+        }
         if (e != hipSuccess) {
-            (void)hipModuleUnload(ctx->mod_gemm);
-            (void)hipModuleUnload(ctx->mod_gemv);
+            unload();
             delete ctx;
             t_hip = e;
             t_msg = std::string("hipModuleGetFunction(") + kKernelNames[k] + "): " + hipGetErrorString(e);
@@ -555,6 +567,76 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     return VX_OK;
 }
 
+// ------------------------------------------------------------ contiguous
+static vx_udiv make_udiv(uint32_t d) {
+    vx_udiv r{};
+    if (d <= 1u) {
+        r.one = 1u;
+        return r;
+    }
+    uint32_t l = 0;
+    while (l < 32u && (1ull << l) < d) ++l;  // ceil(log2 d)
+    r.m = (uint32_t)((((1ull << 32) * ((1ull << l) - d)) / d) + 1ull);
+    r.s = l - 1u;
+    return r;
+}
+
+static int run_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* src,
+                          const uint32_t* dev_offset) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    if (!out || !src) return fail(VX_ERR_INVALID, "null view");
+    // src/linalg/contiguous.rs:43-48: equal size arrays, contiguous output
+    if (std::memcmp(out->layout.size, src->layout.size, sizeof(out->layout.size)) != 0) {
+        static thread_local std::string m;
+        m = "contiguous: tensor size " + layout_str(src->layout) + " differs from output size " + layout_str(out->layout);
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    if (out->layout.rank > 4 || src->layout.rank > 4) return fail(VX_ERR_UNSUPPORTED, "rank > 4");
+    if (!layout_is_contiguous(&out->layout)) {
+        static thread_local std::string m;
+        m = "Output tensor must be contiguous: " + layout_str(out->layout) + ".";
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    vx_layout c;
+    int s = layout_canonicalize(&src->layout, &c);
+    if (s) return s;
+    uint64_t total = 1;
+    for (int i = 0; i < 4; ++i) total *= c.size[i];
+    if (total == 0) return VX_OK;
+    if (total >= (1ull << 32)) return fail(VX_ERR_UNSUPPORTED, "contiguous: 2^32 elements or more");
+    vx_copy_args a{};
+    // Without a device offset the view's own offset is the base shift
+    // (TensorRef::buffer); with one, the raw buffer is read at that offset
+    // (TensorRef::raw_buffer, contiguous.rs:63-71), as the reference does.
+    a.src = (const uint32_t*)src->base + (dev_offset ? 0u : src->layout.offset);
+    a.dst = (uint32_t*)out->base + out->layout.offset;
+    a.dev_offset = dev_offset;
+    for (int i = 0; i < 4; ++i) {
+        a.stride[i] = c.stride[i];
+        a.size[i] = c.size[i];
+    }
+    a.total = (uint32_t)total;
+    a.dw = make_udiv(c.size[3]);
+    a.dh = make_udiv(c.size[2]);
+    a.dc = make_udiv(c.size[1]);
+    DeviceGuard guard(ctx->device);
+    const bool tile = c.stride[2] == 1u && c.stride[3] != 1u && c.size[2] >= 16u && c.size[3] >= 16u;
+    if (tile) {
+        auto cap = [](uint64_t v) { return (uint32_t)(v < 65535u ? v : 65535u); };
+        return launch(ctx, K_vx_contiguous_t64, dim3(cap((c.size[3] + 63u) / 64u), cap((c.size[2] + 63u) / 64u),
+                                                     cap((uint64_t)c.size[0] * c.size[1])),
+                      dim3(256), 0, stream, a);
+    }
+    const bool v4 = !dev_offset && c.stride[3] == 1u && c.size[3] % 4u == 0u && c.stride[0] % 4u == 0u &&
+                    c.stride[1] % 4u == 0u && c.stride[2] % 4u == 0u && aligned16((uintptr_t)a.src) &&
+                    aligned16((uintptr_t)a.dst);
+    uint64_t blocks = ((v4 ? total / 4u : total) + 255u) / 256u;
+    const uint64_t maxb = (uint64_t)ctx->num_cus * 32u;
+    if (blocks > maxb) blocks = maxb;
+    return launch(ctx, v4 ? K_vx_contiguous_v4 : K_vx_contiguous_gen, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+}
+
 static int run_dequant(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     clear_error();
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
@@ -596,8 +678,8 @@ int vx_destroy(vx_ctx ctx) {
     vx::clear_error();
     if (!ctx) return VX_OK;
     vx::DeviceGuard guard(ctx->device);
-    if (ctx->mod_gemm) (void)hipModuleUnload(ctx->mod_gemm);
-    if (ctx->mod_gemv) (void)hipModuleUnload(ctx->mod_gemv);
+    for (hipModule_t m : ctx->mods)
+        if (m) (void)hipModuleUnload(m);
     delete ctx;
     return VX_OK;
 }
@@ -643,6 +725,10 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
 
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     return vx::run_dequant(ctx, stream, out, w);
+}
+
+int vx_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* src, const uint32_t* dev_offset) {
+    return vx::run_contiguous(ctx, stream, out, src, dev_offset);
 }
 
 int vx_qtype_info(uint32_t qtype, uint32_t* block_weights, uint32_t* block_bytes) {

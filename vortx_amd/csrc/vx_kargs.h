@@ -58,4 +58,23 @@ typedef struct vx_gemv_f32_args {
     int64_t a_bs[2], x_bs[2], y_bs[2]; /* batch strides (dims n, c) */
 } vx_gemv_f32_args;
 
+/* Unsigned division by a fixed divisor d >= 1 (round-up multiplier m and
+ * shift s; `one` marks d == 1). */
+typedef struct vx_udiv {
+    uint32_t m, s, one, pad;
+} vx_udiv;
+
+/* Strided -> contiguous copy of 4-byte elements over the canonical
+ * [n, c, h, w] view (strides in elements, 64-bit). */
+typedef struct vx_copy_args {
+    uint32_t* dst;
+    const uint32_t* src;
+    const uint32_t* dev_offset; /* null, or a device u32 added to every source index */
+    int64_t stride[4];
+    uint32_t size[4];
+    uint32_t total;             /* elements (< 2^32) */
+    uint32_t pad0;
+    vx_udiv dw, dh, dc;         /* divisions by size[3], size[2], size[1] */
+} vx_copy_args;
+
 #endif /* VX_KARGS_H */
