@@ -180,6 +180,19 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out,
                   const vx_qweight* w);
 
+/* ---- quantize: f32 -> Q8_0 / Q4_0 / Q4_K -----------------------------
+ * No counterpart in the reference (it has no quantized code): the step
+ * before the GEMV. x is an [rows, cols] f32 view (any strides); the blocks
+ * of row i are written at out->base + i * out->row_stride_bytes. The
+ * algorithms are ggml's reference quantizers (ggml-quants.c
+ * quantize_row_q8_0_ref / quantize_row_q4_0_ref / quantize_row_q4_K_ref,
+ * the latter with make_qkx2_quants), evaluated in their f32 operation order
+ * without contraction, so the bytes equal a sequential CPU run of the same
+ * algorithm. The output must be 2-byte aligned (Q4_K: 4-byte) or
+ * VX_ERR_UNSUPPORTED. Asynchronous on `stream`. */
+int vx_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out,
+                const vx_cview* x);
+
 /* ---- strided -> contiguous copy (4-byte elements) --------------------
  * Replaces Contiguous::launch (src/linalg/contiguous.rs:22-119; shader
  * vortx-shaders/src/linalg/contiguous.rs:59-90): out[i] = src[it(n,c,h,w)]

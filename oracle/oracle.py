@@ -59,6 +59,10 @@ def lib():
         L.orc_max_threads.restype = C.c_int
         L.orc_contiguous_u32.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]
         L.orc_contiguous_u32.restype = C.c_int
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_quantize.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_uint64]
+        L.orc_quantize.restype = C.c_int
         for name in ("orc_dequant", "orc_gemv_q_f64", "orc_gemv_q_f32_omp", "orc_gemm_ref_f32",
                      "orc_gemm_f64", "orc_gemm_tiled_f32_omp", "orc_q4k_scale_min"):
             if name != "orc_q4k_scale_min":
@@ -210,3 +214,23 @@ def contiguous_u32(src_flat: np.ndarray, shape, stride, offset: int = 0) -> np.n
     rc = lib().orc_contiguous_u32(_ptr(out), _ptr(buf), _ptr(size_a), _ptr(st_a), offset)
     assert rc == 0
     return out[:n].reshape(shape) if len(shape) else out[:n]
+
+
+# ------------------------------------------------------------- quantize
+def f32_to_f16(vals) -> np.ndarray:
+    """orc_f32_to_f16 (round to nearest even) over an array; returns uint16 bits."""
+    L = lib()
+    flat = np.asarray(vals, dtype=np.float32).ravel()
+    return np.array([L.orc_f32_to_f16(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(vals))
+
+
+def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
+    """f32 [M, K] -> uint8 [M, row_bytes]: ggml's reference quantizers
+    (quantize_row_{q8_0,q4_0,q4_K}_ref) as restated in vx_oracle.c."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    rb = row_bytes(qtype, K)
+    out = np.zeros((M, rb), dtype=np.uint8)
+    rc = lib().orc_quantize(qtype, _ptr(x), M, K, K, _ptr(out), rb)
+    assert rc == 0, rc
+    return out

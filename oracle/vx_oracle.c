@@ -7,6 +7,15 @@
  *
  * What it restates, and what pins each part (checks live in tests/):
  *
+ *  - orc_quantize: f32 rows -> Q8_0 / Q4_0 / Q4_K blocks, restating ggml's
+ *    published reference quantizers (ggml-quants.c quantize_row_q8_0_ref,
+ *    quantize_row_q4_0_ref, quantize_row_q4_K_ref with make_qkx2_quants and
+ *    nearest_int, in the form they have had since k-quants landed in June
+ *    2023). ggml is not a dependency of vortx and is not in the reference,
+ *    and no ggml-produced vectors exist here, so parity with ggml itself is
+ *    unpinned; the restatement is pinned by invariants (error bounds, exact
+ *    round trips of representable blocks, hand-computed blocks) and
+ *    orc_f32_to_f16 against numpy's float16 rounding.
  *  - orc_contiguous_u32: vortx's contiguous shader (vortx-shaders/src/
  *    linalg/contiguous.rs:59-90): thread i writes dest[i] = src[offset +
  *    it(n, c, h, w)] with (n, c, h, w) the row-major split of i over the
@@ -367,6 +376,219 @@ int orc_contiguous_u32(uint32_t* dest, const uint32_t* src, const uint32_t* size
         const uint32_t w = t % h_stride;
         const uint32_t it = n * stride[0] + c * stride[1] + h * stride[2] + w * stride[3];
         dest[t] = src[offset + it];
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------- quantize */
+/* IEEE binary32 -> binary16, round to nearest even (what ggml's
+ * GGML_FP32_TO_FP16 does with F16C or its software path). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t b;
+    memcpy(&b, &f, 4);
+    const uint32_t sign = (b >> 16) & 0x8000u;
+    const uint32_t exp = (b >> 23) & 0xFFu;
+    uint32_t man = b & 0x7FFFFFu;
+    if (exp == 0xFFu) return (uint16_t)(sign | 0x7C00u | (man ? 0x200u : 0u));
+    const int32_t e = (int32_t)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        uint32_t h = man >> shift;
+        const uint32_t rem = man & ((1u << shift) - 1u), half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (h & 1u))) h += 1u;
+        return (uint16_t)(sign | h);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+    return (uint16_t)(sign | h);
+}
+
+/* ggml nearest_int: round half to even through the 1.5 * 2^23 magic. */
+static int orc_nearest_int(float fval) {
+    const float val = fval + 12582912.f;
+    int32_t i;
+    memcpy(&i, &val, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* ggml make_qkx2_quants (asymmetric 4-bit search over 20 scale candidates,
+ * weighted squared error). */
+static float orc_make_qkx2(int n, int nmax, const float* x, const float* weights, uint8_t* L, float* the_min,
+                           uint8_t* Laux, float rmin, float rdelta, int nstep) {
+    float mn = x[0], mx = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (mn > 0) mn = 0;
+    if (mx == mn) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -mn;
+        return 0.f;
+    }
+    float iscale = nmax / (mx - mn);
+    float scale = 1 / iscale;
+    float best_mad = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = orc_nearest_int(iscale * (x[i] - mn));
+        L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
+        float diff = scale * L[i] + mn - x[i];
+        diff = diff * diff;
+        best_mad += weights[i] * diff;
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (mx - mn);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = orc_nearest_int(iscale * (x[i] - mn));
+            l = l < 0 ? 0 : l > nmax ? nmax : l;
+            Laux[i] = (uint8_t)l;
+            const float w = weights[i];
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * Laux[i] + this_min - x[i];
+                diff = diff * diff;
+                mad += weights[i] * diff;
+            }
+            if (mad < best_mad) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_mad = mad;
+                scale = this_scale;
+                mn = this_min;
+            }
+        }
+    }
+    *the_min = -mn;
+    return scale;
+}
+
+static void orc_put16(uint8_t* p, uint16_t v) {
+    p[0] = (uint8_t)(v & 0xFFu);
+    p[1] = (uint8_t)(v >> 8);
+}
+
+static void orc_quant_q8_0(const float* x, uint8_t* y) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        const float a = fabsf(x[j]);
+        amax = amax > a ? amax : a;
+    }
+    const float d = amax / ((1 << 7) - 1);
+    const float id = d ? 1.0f / d : 0.0f;
+    orc_put16(y, orc_f32_to_f16(d));
+    for (int j = 0; j < 32; ++j) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+}
+
+static void orc_quant_q4_0(const float* x, uint8_t* y) {
+    float amax = 0.0f, mx = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+        const float v = x[j];
+        if (amax < fabsf(v)) {
+            amax = fabsf(v);
+            mx = v;
+        }
+    }
+    const float d = mx / -8;
+    const float id = d ? 1.0f / d : 0.0f;
+    orc_put16(y, orc_f32_to_f16(d));
+    for (int j = 0; j < 16; ++j) {
+        const float x0 = x[j] * id, x1 = x[16 + j] * id;
+        int xi0 = (int8_t)(x0 + 8.5f), xi1 = (int8_t)(x1 + 8.5f);
+        xi0 = xi0 < 15 ? xi0 : 15;
+        xi1 = xi1 < 15 ? xi1 : 15;
+        y[2 + j] = (uint8_t)(xi0 | (xi1 << 4));
+    }
+}
+
+static void orc_quant_q4_k(const float* x, uint8_t* y) {
+    uint8_t L[256], Laux[32];
+    float weights[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = orc_make_qkx2(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    uint8_t* sc = y + 4;
+    memset(sc, 0, 12);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t ls = (uint8_t)orc_nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t)orc_nearest_int(inv_min * mins[j]);
+        ls = ls < 63 ? ls : 63;
+        lm = lm < 63 ? lm : 63;
+        if (j < 4) {
+            sc[j] = ls;
+            sc[j + 4] = lm;
+        } else {
+            sc[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            sc[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            sc[j - 0] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    const uint16_t dh = orc_f32_to_f16(max_scale / 63.f), mh = orc_f32_to_f16(max_min / 63.f);
+    orc_put16(y, dh);
+    orc_put16(y + 2, mh);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t scv, mv;
+        orc_q4k_scale_min(sc, j, &scv, &mv);
+        const float d = orc_f16_to_f32(dh) * scv;
+        if (!d) continue;
+        const float dm = orc_f16_to_f32(mh) * mv;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = orc_nearest_int((x[32 * j + ii] + dm) / d);
+            l = l < 0 ? 0 : l > 15 ? 15 : l;
+            L[32 * j + ii] = (uint8_t)l;
+        }
+    }
+    uint8_t* q = y + 16;
+    for (int j = 0; j < 256; j += 64) {
+        for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+        q += 32;
+    }
+}
+
+/* x: M rows of K f32 (row i at x + i * x_row_stride elements); out: M rows
+ * of blocks, row_stride_bytes apart. K must be a multiple of the block. */
+int orc_quantize(uint32_t qtype, const float* x, uint32_t M, uint32_t K, uint64_t x_row_stride, uint8_t* out,
+                 uint64_t row_stride_bytes) {
+    uint32_t qk, bb;
+    if (orc_qtype_info(qtype, &qk, &bb)) return -1;
+    if (K % qk) return -2;
+    for (uint32_t i = 0; i < M; ++i) {
+        const float* xr = x + (uint64_t)i * x_row_stride;
+        uint8_t* yr = out + (uint64_t)i * row_stride_bytes;
+        for (uint32_t b = 0; b < K / qk; ++b) {
+            if (qtype == 8) orc_quant_q8_0(xr + (uint64_t)b * 32, yr + (uint64_t)b * 34);
+            else if (qtype == 2) orc_quant_q4_0(xr + (uint64_t)b * 32, yr + (uint64_t)b * 18);
+            else orc_quant_q4_k(xr + (uint64_t)b * 256, yr + (uint64_t)b * 144);
+        }
     }
     return 0;
 }

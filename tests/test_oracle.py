@@ -242,3 +242,81 @@ def test_oracle_canonicalize_rule():
     """src/shapes.rs:145-155: leading size-1 dims with contiguous strides."""
     assert O.canonicalize((5, 6), (1, 5)) == ([1, 1, 5, 6], [30, 30, 1, 5])
     assert O.canonicalize((2, 3, 4, 5), (9, 8, 7, 6)) == ([2, 3, 4, 5], [9, 8, 7, 6])
+
+
+# ---------------------------------------------------------------- quantize
+def test_oracle_f32_to_f16_matches_numpy():
+    """orc_f32_to_f16 is IEEE round-to-nearest-even: numpy's float16 cast on
+    random magnitudes from 1e-9 to 1e5, ties, subnormals and the overflow edge."""
+    rng = np.random.default_rng(11)
+    vals = (rng.standard_normal(20000) * 10.0 ** rng.uniform(-9, 5, 20000)).astype(np.float32)
+    edges = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e9, np.inf, -np.inf, 2.0 ** -24, 2.0 ** -25,
+                      1.5 * 2.0 ** -24, 2.5 * 2.0 ** -24, 6.1e-5, -6.1e-5, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11],
+                     dtype=np.float32)
+    allv = np.concatenate([vals, edges])
+    with np.errstate(over="ignore"):
+        ref = allv.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.f32_to_f16(allv), ref)
+
+
+def _block(qtype, x):
+    return O.quantize(qtype, np.asarray(x, dtype=np.float32).reshape(1, -1))[0]
+
+
+def test_quantize_q8_0_known_block():
+    """amax = 127/16 makes d = 1/16 exactly, so every q = 16 x is exact."""
+    q = np.array([127, -127, 0, 1, -1, 64, -64, 100] * 4, dtype=np.int8)
+    blk = _block(O.Q8_0, q.astype(np.float32) / 16.0)
+    assert blk[:2].tobytes() == np.float16(1 / 16).tobytes()
+    assert np.array_equal(blk[2:].view(np.int8), q)
+
+
+def test_quantize_q4_0_known_block():
+    """x = (q - 8) d with the extreme -8 d present: d and the nibbles come
+    back exactly (qs byte j = q_j | q_{j+16} << 4)."""
+    q = np.array([0, 15, 8, 3, 12, 7, 9, 1] * 4, dtype=np.int32)
+    d = 0.25
+    blk = _block(O.Q4_0, (q - 8) * d)
+    assert blk[:2].tobytes() == np.float16(d).tobytes()
+    expect = (q[:16] | (q[16:] << 4)).astype(np.uint8)
+    assert np.array_equal(blk[2:], expect)
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K])
+def test_quantize_zero_and_requantize_invariants(qtype):
+    qk, bb = O.QTYPE_INFO[qtype]
+    zero = O.quantize(qtype, np.zeros((2, 2 * qk), np.float32))
+    assert not O.dequant(qtype, zero, 2, 2 * qk).any(), "an all-zero block decodes to zeros"
+    if qtype == O.Q4_0:
+        # d = max / -8 = -0.0 (f16 0x8000) and every nibble is 8 (value 0)
+        blocks = zero.reshape(-1, bb)
+        assert (blocks[:, :2] == [0x00, 0x80]).all() and (blocks[:, 2:] == 0x88).all()
+    else:
+        assert not zero.any()
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((24, 1024)).astype(np.float32)
+    q = O.quantize(qtype, x)
+    dq = O.dequant(qtype, q, 24, 1024)
+    q2 = O.quantize(qtype, dq)
+    if qtype != O.Q4_K:
+        # a dequantized matrix is a fixed point of the symmetric quantizers
+        assert np.array_equal(q2, q)
+    else:
+        # Q4_K's scale/min search (20 candidate steps, then 6-bit rounding of the
+        # super-block scales) lands on the same blocks for most inputs but is not
+        # a projection; requantizing must stay close to the first decode
+        same = (q2.reshape(-1, bb) == q.reshape(-1, bb)).all(axis=1).mean()
+        assert same >= 0.95
+        dq2 = O.dequant(qtype, q2, 24, 1024)
+        assert np.sqrt(((dq2 - dq) ** 2).mean()) <= 0.01 * np.sqrt((dq ** 2).mean())
+    # error bounds per block: Q8_0 <= 0.5 d + 127 |d - d16|; Q4_0 <= |d| (d = -max/8 maps the
+    # extreme to -8; the opposite side is clamped at +7, one step short of +8) + f16 rounding of d
+    err = np.abs(dq - x).reshape(24, -1, 32)
+    amax = np.abs(x).reshape(24, -1, 32).max(axis=2)
+    if qtype == O.Q8_0:
+        assert (err.max(axis=2) <= amax / 127 * (0.5 + 127 * 2.0 ** -11) * 1.0001).all()
+    elif qtype == O.Q4_0:
+        assert (err.max(axis=2) <= amax / 8 * (1.0 + 8 * 2.0 ** -11) * 1.0001).all()
+    else:
+        # 4-bit asymmetric with 6-bit scales: rms error of gaussian data ~ 7 %
+        assert np.sqrt((err ** 2).mean()) <= 0.09 * np.sqrt((x ** 2).mean())

@@ -233,6 +233,12 @@ class QuantGemv(_Context):
         flags = _ffi.VX_GEMV_X_INT8 if x_int8 else 0
         check(lib().vx_gemv_q_ex(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags))
 
+    def quantize(self, out: "QWeight", x, stream=None) -> None:
+        """Write the blocks of ``out`` from the f32 [rows, cols] view ``x``
+        (ggml's reference quantizers; see include/vortx_hip.h vx_quantize)."""
+        xv, wc = _view_of(x, False), out._c()
+        check(lib().vx_quantize(self._h, _stream(stream), C.byref(wc), C.byref(xv)))
+
     def dequantize(self, out, w: QWeight, stream=None) -> None:
         ov, wc = _view_of(out, True), w._c()
         check(lib().vx_dequantize(self._h, _stream(stream), C.byref(ov), C.byref(wc)))

@@ -48,6 +48,7 @@ SIGNATURES = [
     ("vx_gemv_q", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView)]),
     ("vx_gemv_q_ex", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView), C.c_uint32]),
     ("vx_dequantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight)]),
+    ("vx_quantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxQWeight), _P(VxCView)]),
     ("vx_contiguous", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), C.c_void_p]),
     ("vx_qtype_info", C.c_int, [C.c_uint32, _P(C.c_uint32), _P(C.c_uint32)]),
     ("vx_layout_contiguous", C.c_int, [_P(C.c_uint32), C.c_uint32, _P(VxLayout)]),

@@ -1,0 +1,274 @@
+// quantize.hip — f32 rows -> GGML Q8_0 / Q4_0 / Q4_K blocks for gfx950.
+//
+// The algorithms are ggml's reference quantizers (ggml-quants.c:
+// quantize_row_q8_0_ref, quantize_row_q4_0_ref, quantize_row_q4_K_ref with
+// make_qkx2_quants and nearest_int), evaluated in the same f32 operation
+// order with no contraction (the pragma below), IEEE division and square
+// root, round-to-nearest-even f32 -> f16: the blocks equal those of a
+// sequential CPU run of the same algorithm bit for bit. The reference
+// (vortx) has no quantized code; this is the step before its GEMV.
+//
+//   vx_quantize_q8_0 / _q4_0  one lane per 32-block (HBM-bound);
+//   vx_quantize_q4_k          8 lanes per 256-super-block, lane j running
+//                             the scale/min search of sub-block j, the
+//                             lanes meeting through shuffles for the
+//                             super-block maxima, the 6-bit scale packing
+//                             and the nibble pairs (compute-bound: about
+//                             20 search passes of 32 elements per lane).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../vx_kargs.h"
+
+#pragma clang fp contract(off)
+
+typedef float f32x4q __attribute__((ext_vector_type(4)));
+
+// The empty asm pins v as an already-rounded f32: without it the backend folds
+// a preceding multiply into v_fma_mix (one rounding straight to f16, and a
+// +0 addend that turns -0 into +0), which is not ggml's f32 -> f16 of an f32.
+__device__ __forceinline__ uint16_t vx_f32_to_f16_bits(float v) {
+    asm("" : "+v"(v));
+    return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32, round to nearest even
+}
+__device__ __forceinline__ float vx_f16_bits_to_f32(uint32_t b) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(b & 0xFFFFu));
+}
+
+// ggml nearest_int: round half to even through the 1.5 * 2^23 magic.
+__device__ __forceinline__ int vx_nearest_int(float fval) {
+    const float val = fval + 12582912.f;
+    return (int)(__builtin_bit_cast(uint32_t, val) & 0x007fffffu) - 0x00400000;
+}
+
+__device__ __forceinline__ void vx_q_load32(const vx_quant_args& a, uint32_t row, uint32_t k0, float (&x)[32]) {
+    const float* xr = a.x + (int64_t)row * a.xs_m;
+    if (a.x_vec) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4q v = *(const f32x4q*)(xr + k0 + 4 * i);
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) x[i] = xr[(int64_t)(k0 + i) * a.xs_k];
+    }
+}
+
+// grid: x covers the blocks of a row (256 per workgroup), y the rows (loop).
+extern "C" __global__ __launch_bounds__(256) void vx_quantize_q8_0(vx_quant_args a) {
+    const uint32_t b = blockIdx.x * 256u + threadIdx.x;
+    if (b >= a.nblk) return;
+    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
+        float x[32];
+        vx_q_load32(a, row, 32u * b, x);
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const float v = fabsf(x[j]);
+            amax = amax > v ? amax : v;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint16_t* y = (uint16_t*)(a.out + (uint64_t)row * a.row_stride + 34ull * b);
+        y[0] = vx_f32_to_f16_bits(d);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t q0 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j] * id);
+            const uint32_t q1 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j + 1] * id);
+            y[1 + j] = (uint16_t)(q0 | (q1 << 8));
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_0(vx_quant_args a) {
+    const uint32_t b = blockIdx.x * 256u + threadIdx.x;
+    if (b >= a.nblk) return;
+    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
+        float x[32];
+        vx_q_load32(a, row, 32u * b, x);
+        float amax = 0.0f, mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            if (amax < fabsf(x[j])) {
+                amax = fabsf(x[j]);
+                mx = x[j];
+            }
+        }
+        const float d = mx / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint16_t* y = (uint16_t*)(a.out + (uint64_t)row * a.row_stride + 18ull * b);
+        y[0] = vx_f32_to_f16_bits(d);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t pr = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int jj = 2 * j + t;
+                int xi0 = (int8_t)(x[jj] * id + 8.5f);
+                int xi1 = (int8_t)(x[16 + jj] * id + 8.5f);
+                xi0 = xi0 < 15 ? xi0 : 15;
+                xi1 = xi1 < 15 ? xi1 : 15;
+                pr |= (uint32_t)(xi0 | (xi1 << 4)) << (8 * t);
+            }
+            y[1 + j] = (uint16_t)pr;
+        }
+    }
+}
+
+// make_qkx2_quants(32, 15, x, weights, L, &min, Laux, -1, 0.1, 20, false)
+__device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float (&w)[32], uint8_t (&L)[32],
+                                              float& the_min) {
+    const int nmax = 15;
+    const float rmin = -1.f, rdelta = 0.1f;
+    const int nstep = 20;
+    float mn = x[0], mx = x[0];
+    float sum_w = w[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < 32; ++i) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
+        sum_w += w[i];
+        sum_x += w[i] * x[i];
+    }
+    if (mn > 0) mn = 0;
+    if (mx == mn) {
+        for (int i = 0; i < 32; ++i) L[i] = 0;
+        the_min = -mn;
+        return 0.f;
+    }
+    float iscale = (float)nmax / (mx - mn);
+    float scale = 1 / iscale;
+    float best_mad = 0;
+    for (int i = 0; i < 32; ++i) {
+        const int l = vx_nearest_int(iscale * (x[i] - mn));
+        L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
+        float diff = scale * (float)L[i] + mn - x[i];
+        diff = diff * diff;
+        best_mad += w[i] * diff;
+    }
+    uint8_t Laux[32];
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * (float)is + (float)nmax) / (mx - mn);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < 32; ++i) {
+            int l = vx_nearest_int(iscale * (x[i] - mn));
+            l = l < 0 ? 0 : l > nmax ? nmax : l;
+            Laux[i] = (uint8_t)l;
+            const float fl = (float)l;
+            sum_l += w[i] * fl;
+            sum_l2 += w[i] * fl * fl;
+            sum_xl += w[i] * fl * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+            for (int i = 0; i < 32; ++i) {
+                float diff = this_scale * (float)Laux[i] + this_min - x[i];
+                diff = diff * diff;
+                mad += w[i] * diff;
+            }
+            if (mad < best_mad) {
+                for (int i = 0; i < 32; ++i) L[i] = Laux[i];
+                best_mad = mad;
+                scale = this_scale;
+                mn = this_min;
+            }
+        }
+    }
+    the_min = -mn;
+    return scale;
+}
+
+// 8 lanes per super-block (lane j = sub-block j); 256 threads = 32
+// super-blocks. grid: x covers the super-blocks of a row, y the rows.
+extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args a) {
+    const uint32_t j = threadIdx.x & 7u;
+    const uint32_t sb = blockIdx.x * 32u + (threadIdx.x >> 3);
+    const bool live = sb < a.nblk;  // whole 8-lane groups agree
+    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
+        float x[32], w[32];
+        uint8_t L[32];
+        float scale = 0.f, mn = 0.f;
+        if (live) {
+            vx_q_load32(a, row, 256u * sb + 32u * j, x);
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+            const float av_x = __builtin_sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
+            scale = vx_make_qkx2(x, w, L, mn);
+        }
+        // super-block maxima (ggml starts both at 0)
+        float max_scale = scale > 0.f ? scale : 0.f, max_min = mn > 0.f ? mn : 0.f;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            const float s2 = __shfl_xor(max_scale, o, 64), m2 = __shfl_xor(max_min, o, 64);
+            max_scale = s2 > max_scale ? s2 : max_scale;
+            max_min = m2 > max_min ? m2 : max_min;
+        }
+        const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+        const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+        uint32_t ls = (uint32_t)(uint8_t)vx_nearest_int(inv_scale * scale);
+        uint32_t lm = (uint32_t)(uint8_t)vx_nearest_int(inv_min * mn);
+        ls = ls < 63u ? ls : 63u;
+        lm = lm < 63u ? lm : 63u;
+        const uint16_t dh = vx_f32_to_f16_bits(max_scale / 63.f), mh = vx_f32_to_f16_bits(max_min / 63.f);
+        // the 6-bit pair (ls, lm) round-trips through the packing unchanged
+        const float dq = vx_f16_bits_to_f32(dh) * (float)ls;
+        if (live && dq != 0.f) {
+            const float dm = vx_f16_bits_to_f32(mh) * (float)lm;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = vx_nearest_int((x[ii] + dm) / dq);
+                L[ii] = (uint8_t)(l < 0 ? 0 : l > 15 ? 15 : l);
+            }
+        }
+        // scales[12]: j < 4: sc[j] = ls_j | (ls_{j+4} >> 4) << 6,
+        // sc[j+4] = lm_j | (lm_{j+4} >> 4) << 6; j >= 4: sc[j+4] = (ls_j & 15) | (lm_j & 15) << 4
+        const uint32_t ls4 = (uint32_t)__shfl_xor((int)ls, 4, 64), lm4 = (uint32_t)__shfl_xor((int)lm, 4, 64);
+        uint32_t Lp[4];  // this lane's 32 nibbles, 8 per dword
+#pragma unroll
+        for (int d4 = 0; d4 < 4; ++d4) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) v |= (uint32_t)L[8 * d4 + t] << (4 * t);
+            Lp[d4] = v;
+        }
+        uint32_t Lh[4];  // the odd partner's nibbles (sub-block 2c + 1)
+#pragma unroll
+        for (int d4 = 0; d4 < 4; ++d4) Lh[d4] = (uint32_t)__shfl_xor((int)Lp[d4], 1, 64);
+        if (!live) continue;
+        uint8_t* yb = a.out + (uint64_t)row * a.row_stride + 144ull * sb;
+        if (j == 0) {
+            ((uint16_t*)yb)[0] = dh;
+            ((uint16_t*)yb)[1] = mh;
+        }
+        if (j < 4) {
+            yb[4 + j] = (uint8_t)(ls | ((ls4 >> 4) << 6));
+            yb[8 + j] = (uint8_t)(lm | ((lm4 >> 4) << 6));
+        } else {
+            yb[8 + j] = (uint8_t)((ls & 15u) | ((lm & 15u) << 4));
+        }
+        if ((j & 1u) == 0u) {
+            // chunk c = j / 2: byte l = L_{2c}[l] | L_{2c+1}[l] << 4
+            uint32_t* q = (uint32_t*)(yb + 16u + 16u * j);
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int l = 4 * d + t;
+                    const uint32_t lo = (Lp[l >> 3] >> (4 * (l & 7))) & 15u;
+                    const uint32_t hi = (Lh[l >> 3] >> (4 * (l & 7))) & 15u;
+                    v |= (lo | (hi << 4)) << (8 * t);
+                }
+                q[d] = v;
+            }
+        }
+    }
+}

@@ -28,6 +28,8 @@ extern const unsigned char vx_co_gemv_q[];
 extern const unsigned char vx_co_gemv_q_end[];
 extern const unsigned char vx_co_copy[];
 extern const unsigned char vx_co_copy_end[];
+extern const unsigned char vx_co_quantize[];
+extern const unsigned char vx_co_quantize_end[];
 }
 
 namespace vx {
@@ -66,8 +68,8 @@ static const char* const kKernelNames[K_COUNT] = {
 #undef K
 };
 // The embedded code objects; every kernel name is unique across them.
-static const unsigned char* const kModules[] = {vx_co_gemm, vx_co_gemv_q, vx_co_copy};
-constexpr int kNumModules = 3;
+static const unsigned char* const kModules[] = {vx_co_gemm, vx_co_gemv_q, vx_co_copy, vx_co_quantize};
+constexpr int kNumModules = 4;
 
 }  // namespace vx
 
@@ -637,6 +639,40 @@ static int run_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out, con
     return launch(ctx, v4 ? K_vx_contiguous_v4 : K_vx_contiguous_gen, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
 }
 
+// ------------------------------------------------------------- quantize
+static int run_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, const vx_cview* x) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    uint32_t qk, bb;
+    int s = check_qweight(out, &qk, &bb);
+    if (s) return s;
+    if (!x) return fail(VX_ERR_INVALID, "null view");
+    if (x->layout.rank != 2) return fail(VX_ERR_SHAPE, "quantize input must be a rank-2 [M, K] view");
+    Canon cx;
+    if ((s = canon_view(x->base, &x->layout, &cx, "x"))) return s;
+    if (cx.l.size[2] != out->rows || cx.l.size[3] != out->cols) return fail(VX_ERR_SHAPE, "input view is not [rows, cols]");
+    if (out->rows == 0 || out->cols == 0) return VX_OK;
+    // block stores: 16-bit (Q8_0, Q4_0) or 32-bit (Q4_K)
+    const uint64_t al = out->qtype == VX_Q4_K ? 4u : 2u;
+    if (((uintptr_t)out->base % al) || (out->row_stride_bytes % al))
+        return fail(VX_ERR_UNSUPPORTED, "quantize output must be 2-byte (Q4_K: 4-byte) aligned");
+    vx_quant_args a{};
+    a.x = (const float*)cx.ptr;
+    a.xs_m = cx.l.stride[2];
+    a.xs_k = cx.l.stride[3];
+    a.out = (uint8_t*)out->base;
+    a.row_stride = out->row_stride_bytes;
+    a.M = out->rows;
+    a.K = out->cols;
+    a.nblk = out->cols / qk;
+    a.x_vec = (a.xs_k == 1 && aligned16(cx.ptr) && a.xs_m % 4 == 0) ? 1u : 0u;
+    DeviceGuard guard(ctx->device);
+    const uint32_t gy = a.M < 65535u ? a.M : 65535u;
+    if (out->qtype == VX_Q4_K) return launch(ctx, K_vx_quantize_q4_k, dim3((a.nblk + 31u) / 32u, gy), dim3(256), 0, stream, a);
+    return launch(ctx, out->qtype == VX_Q8_0 ? K_vx_quantize_q8_0 : K_vx_quantize_q4_0, dim3((a.nblk + 255u) / 256u, gy),
+                  dim3(256), 0, stream, a);
+}
+
 static int run_dequant(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     clear_error();
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
@@ -725,6 +761,10 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
 
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     return vx::run_dequant(ctx, stream, out, w);
+}
+
+int vx_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, const vx_cview* x) {
+    return vx::run_quantize(ctx, stream, out, x);
 }
 
 int vx_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* src, const uint32_t* dev_offset) {

@@ -77,4 +77,15 @@ typedef struct vx_copy_args {
     vx_udiv dw, dh, dc;         /* divisions by size[3], size[2], size[1] */
 } vx_copy_args;
 
+/* f32 [M, K] -> quantized blocks (row i at out + i * row_stride). */
+typedef struct vx_quant_args {
+    const float* x;
+    int64_t xs_m, xs_k;
+    uint8_t* out;
+    uint64_t row_stride;
+    uint32_t M, K;
+    uint32_t nblk;   /* blocks (Q4_K: super-blocks) per row */
+    uint32_t x_vec;  /* 1: xs_k == 1 and 16-byte aligned rows */
+} vx_quant_args;
+
 #endif /* VX_KARGS_H */
