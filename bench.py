@@ -175,6 +175,37 @@ def time_contiguous(shape, steps: int, warmup: int):
             "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
 
 
+def time_quantize(qtype: int, M: int, K: int, steps: int, warmup: int):
+    """ggml's reference quantizer (quantize_row_*_ref) of an f32 [M, K] matrix
+    into blocks: bytes = 4 M K read + the blocks written; 2 rotating inputs of
+    4 M K bytes each (>= 256 MB together at 14336x4096)."""
+    import torch
+
+    import vortx_amd as vx
+
+    dev = torch.device("cuda:0")
+    qk, bb = vx.qtype_info(qtype)
+    xs = [torch.randn((M, K), device=dev) for _ in range(2)]
+    buf = torch.empty(M * (K // qk) * bb, dtype=torch.uint8, device=dev)
+    w = vx.QWeight(buf, qtype, M, K)
+    qg = vx.QuantGemv(0)
+    for i in range(warmup):
+        qg.quantize(w, xs[i % 2])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        qg.quantize(w, xs[i % 2])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    nbytes = 4 * M * K + buf.numel()
+    return {"value": nbytes * steps / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / steps,
+            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
+
+
 def cpu_baselines(threads: int):
     """Oracle OpenMP restatements on the host cores (bounded samples)."""
     import numpy as np
@@ -247,6 +278,11 @@ def main() -> int:
     log(f"[gemm] {gemm}")
     cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
     log(f"[contiguous] {cont}")
+    quant = []
+    for qt, label in ((8, "q8_0"), (12, "q4_k")):
+        r = time_quantize(qt, 14336, 4096, max(10, args.steps // (20 if qt == 8 else 100)), 3)
+        log(f"[quantize_{label}] {r}")
+        quant.append((label, r))
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     cpu = None if args.no_cpu else cpu_baselines(threads)
@@ -284,6 +320,14 @@ def main() -> int:
             {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
              "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],
              "roofline": roof_hbm(cont, "contiguous_t8192")},
+        ] + [
+            {"workload": f"quantize f32 14336x4096 to {label.upper()} blocks (ggml reference quantizer)",
+             "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
+             "roofline": roof_hbm(r, f"quantize_{label}_14336x4096"),
+             **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block"}
+                if label == "q4_k" else {})}
+            for label, r in quant
+        ] + [
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
              "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",

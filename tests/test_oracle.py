@@ -282,6 +282,45 @@ def test_quantize_q4_0_known_block():
     assert np.array_equal(blk[2:], expect)
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_quantize_q4_k_exact_grid_known_answer(seed):
+    """Sub-block j holds x = s_j q - m_j with power-of-two s_j, m_j in {0, s_j/2, s_j, 2 s_j}
+    and both q = 0 and q = 15 present. Then max - min = 15 s_j exactly, so the search's
+    first candidate (iscale = 15 / (max - min)) reproduces q with zero error and no later
+    candidate can be strictly better: the sub-block fit is (s_j, m_j) exactly. What follows
+    is ggml's super-block step in closed form (d = f16(max s / 63), dmin = f16(max m / 63),
+    6-bit scales = rne(63 s_j / max s), the same for mins) and a requantization that
+    returns q (asserted below from the f16 scales themselves). Pins the 6-bit scale and
+    nibble packing, the f16 rounding and the requantization independently of the search."""
+    rng = np.random.default_rng(seed)
+    e = rng.integers(-6, 0, 8)
+    e[rng.integers(0, 8)] = e.max() - 4  # one sub-block 16x smaller: a 6-bit scale of 4
+    s = np.ldexp(np.float32(1), e).astype(np.float32)
+    m = (s * rng.choice([0.0, 0.5, 1.0, 2.0], 8)).astype(np.float32)
+    q = rng.integers(0, 16, (8, 32))
+    q[:, 0], q[:, 1] = 0, 15
+    x = (s[:, None] * q - m[:, None]).astype(np.float32)
+    assert np.array_equal((x + m[:, None]) / s[:, None], q), "grid values are exact in f32"
+    blk = _block(O.Q4_K, x.reshape(-1))
+    f32 = np.float32
+    max_s, max_m = s.max(), m.max()
+    d16, dm16 = np.float16(f32(max_s) / f32(63)), np.float16(f32(max_m) / f32(63))
+    assert blk[0:2].tobytes() == d16.tobytes() and blk[2:4].tobytes() == dm16.tobytes()
+    inv_s = f32(63) / max_s
+    inv_m = f32(63) / max_m if max_m > 0 else f32(0)
+    ls = np.minimum(np.rint(inv_s * s), 63).astype(int)  # rint: half to even, like nearest_int
+    lm = np.minimum(np.rint(inv_m * m), 63).astype(int)
+    for j in range(8):
+        assert O.q4k_scale_min(bytes(blk[4:16]), j) == (ls[j], lm[j]), j
+    # requantization nearest_int((x + dmin lm) / (d ls)) lands on q with margin
+    dq = np.float64(d16) * ls
+    dm = np.float64(dm16) * lm
+    r = (x.astype(np.float64) + dm[:, None]) / dq[:, None]
+    assert np.abs(r - q).max() < 0.45
+    qs = blk[16:].reshape(4, 32)
+    assert np.array_equal(qs & 15, q[0::2]) and np.array_equal(qs >> 4, q[1::2])
+
+
 @pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q4_K])
 def test_quantize_zero_and_requantize_invariants(qtype):
     qk, bb = O.QTYPE_INFO[qtype]

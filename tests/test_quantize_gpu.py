@@ -36,6 +36,26 @@ def _edge_rows(K, rng):
     return np.stack(rows)
 
 
+def _grid_rows(M, K, rng):
+    """Super-blocks of exact grids x = s q - m (power-of-two s, m in {0, s/2, s, 2s},
+    q = 0 and 15 in every 32): the Q4_K search's first candidate is an exact fit."""
+    e = rng.integers(-8, 0, (M, K // 32))
+    s = np.ldexp(np.float32(1), e).astype(np.float32)
+    m = s * rng.choice(np.float32([0.0, 0.5, 1.0, 2.0]), (M, K // 32))
+    q = rng.integers(0, 16, (M, K // 32, 32))
+    q[:, :, 0], q[:, :, 1] = 0, 15
+    return (s[..., None] * q - m[..., None]).astype(np.float32).reshape(M, K)
+
+
+def _tie_rows(M, K, rng):
+    """Blocks whose max is 127/16 (Q8_0: id = 16 exactly) and whose other values are
+    odd multiples of 1/32, so x * id lands exactly on k + 1/2: rounding ties."""
+    k = rng.integers(-127, 127, (M, K)).astype(np.float32)
+    x = (k + np.float32(0.5)) / np.float32(16)
+    x[:, ::32] = np.float32(127 / 16) * rng.choice(np.float32([-1, 1]), (M, K // 32))
+    return x.astype(np.float32)
+
+
 def _run(qg, qtype, x_np, strided=False):
     M, K = x_np.shape
     rb = S.row_bytes(qtype, K)
@@ -52,7 +72,7 @@ def _run(qg, qtype, x_np, strided=False):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
-@pytest.mark.parametrize("dist", ["normal", "uniform", "edges"])
+@pytest.mark.parametrize("dist", ["normal", "uniform", "edges", "grid", "ties"])
 def test_quantize_bytes_match_oracle(qgemv, qtype, dist):
     rng = np.random.default_rng(41)
     K = 1024
@@ -60,6 +80,10 @@ def test_quantize_bytes_match_oracle(qgemv, qtype, dist):
         x = rng.standard_normal((37, K)).astype(np.float32)
     elif dist == "uniform":
         x = rng.uniform(-1, 1, (37, K)).astype(np.float32)
+    elif dist == "grid":
+        x = _grid_rows(16, K, rng)
+    elif dist == "ties":
+        x = _tie_rows(16, K, rng)
     else:
         x = _edge_rows(K, rng)
     note(f"quantize {QN[qtype]} {dist}")

@@ -116,8 +116,17 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_0(vx_quant_args
     }
 }
 
-// make_qkx2_quants(32, 15, x, weights, L, &min, Laux, -1, 0.1, 20, false)
-__device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float (&w)[32], uint8_t (&L)[32],
+// make_qkx2_quants(32, 15, x, weights, L, &min, Laux, -1, 0.1, 20, false).
+// Every loop over the 32 values is unrolled so x, w and the candidate levels
+// stay in registers (a rolled loop indexes them through 32-way selects).
+// Instead of copying the winning candidate's levels on each improvement, the
+// (iscale, min) pair that produced them is kept and the levels are rebuilt
+// once by vx_qkx2_levels: the same nearest_int(iscale * (x - min)), clamped.
+struct vx_qkx2_best {
+    float iscale, mnu;  // the winning candidate's inputs; iscale 0 = all levels 0
+};
+
+__device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float (&w)[32], vx_qkx2_best& best,
                                               float& the_min) {
     const int nmax = 15;
     const float rmin = -1.f, rdelta = 0.1f;
@@ -125,6 +134,7 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
     float mn = x[0], mx = x[0];
     float sum_w = w[0];
     float sum_x = sum_w * x[0];
+#pragma unroll
     for (int i = 1; i < 32; ++i) {
         if (x[i] < mn) mn = x[i];
         if (x[i] > mx) mx = x[i];
@@ -133,32 +143,36 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
     }
     if (mn > 0) mn = 0;
     if (mx == mn) {
-        for (int i = 0; i < 32; ++i) L[i] = 0;
+        best.iscale = 0.f;
+        best.mnu = 0.f;
         the_min = -mn;
         return 0.f;
     }
     float iscale = (float)nmax / (mx - mn);
     float scale = 1 / iscale;
     float best_mad = 0;
+    best.iscale = iscale;
+    best.mnu = mn;
+#pragma unroll
     for (int i = 0; i < 32; ++i) {
         const int l = vx_nearest_int(iscale * (x[i] - mn));
-        L[i] = (uint8_t)(l < 0 ? 0 : l > nmax ? nmax : l);
-        float diff = scale * (float)L[i] + mn - x[i];
+        const float fl = (float)(l < 0 ? 0 : l > nmax ? nmax : l);
+        float diff = scale * fl + mn - x[i];
         diff = diff * diff;
         best_mad += w[i] * diff;
     }
-    uint8_t Laux[32];
+    float fl[32];
     for (int is = 0; is <= nstep; ++is) {
         iscale = (rmin + rdelta * (float)is + (float)nmax) / (mx - mn);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+#pragma unroll
         for (int i = 0; i < 32; ++i) {
             int l = vx_nearest_int(iscale * (x[i] - mn));
             l = l < 0 ? 0 : l > nmax ? nmax : l;
-            Laux[i] = (uint8_t)l;
-            const float fl = (float)l;
-            sum_l += w[i] * fl;
-            sum_l2 += w[i] * fl * fl;
-            sum_xl += w[i] * fl * x[i];
+            fl[i] = (float)l;
+            sum_l += w[i] * fl[i];
+            sum_l2 += w[i] * fl[i] * fl[i];
+            sum_xl += w[i] * fl[i] * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
         if (D > 0) {
@@ -169,13 +183,15 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
                 this_scale = sum_xl / sum_l2;
             }
             float mad = 0;
+#pragma unroll
             for (int i = 0; i < 32; ++i) {
-                float diff = this_scale * (float)Laux[i] + this_min - x[i];
+                float diff = this_scale * fl[i] + this_min - x[i];
                 diff = diff * diff;
                 mad += w[i] * diff;
             }
             if (mad < best_mad) {
-                for (int i = 0; i < 32; ++i) L[i] = Laux[i];
+                best.iscale = iscale;
+                best.mnu = mn;
                 best_mad = mad;
                 scale = this_scale;
                 mn = this_min;
@@ -186,23 +202,38 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
     return scale;
 }
 
+// The levels make_qkx2_quants leaves in L for the winning candidate.
+__device__ __forceinline__ void vx_qkx2_levels(const float (&x)[32], const vx_qkx2_best& best, uint8_t (&L)[32]) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int l = best.iscale == 0.f ? 0 : vx_nearest_int(best.iscale * (x[i] - best.mnu));
+        L[i] = (uint8_t)(l < 0 ? 0 : l > 15 ? 15 : l);
+    }
+}
+
 // 8 lanes per super-block (lane j = sub-block j); 256 threads = 32
-// super-blocks. grid: x covers the super-blocks of a row, y the rows.
+// super-blocks of the flattened (row, super-block) sequence; grid-stride.
 extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args a) {
     const uint32_t j = threadIdx.x & 7u;
-    const uint32_t sb = blockIdx.x * 32u + (threadIdx.x >> 3);
-    const bool live = sb < a.nblk;  // whole 8-lane groups agree
-    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
+    const uint64_t total = (uint64_t)a.M * a.nblk;
+    for (uint64_t g0 = (uint64_t)blockIdx.x * 32u; g0 < total; g0 += (uint64_t)gridDim.x * 32u) {
+        const uint64_t g = g0 + (threadIdx.x >> 3);
+        const bool live = g < total;  // whole 8-lane groups agree
+        const uint32_t row = live ? (uint32_t)(g / a.nblk) : 0u;
+        const uint32_t sb = live ? (uint32_t)(g - (uint64_t)row * a.nblk) : 0u;
         float x[32], w[32];
         uint8_t L[32];
+        vx_qkx2_best best{0.f, 0.f};
         float scale = 0.f, mn = 0.f;
         if (live) {
             vx_q_load32(a, row, 256u * sb + 32u * j, x);
             float sum_x2 = 0;
+#pragma unroll
             for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
             const float av_x = __builtin_sqrtf(sum_x2 / 32);
+#pragma unroll
             for (int l = 0; l < 32; ++l) w[l] = av_x + fabsf(x[l]);
-            scale = vx_make_qkx2(x, w, L, mn);
+            scale = vx_make_qkx2(x, w, best, mn);
         }
         // super-block maxima (ggml starts both at 0)
         float max_scale = scale > 0.f ? scale : 0.f, max_min = mn > 0.f ? mn : 0.f;
@@ -223,10 +254,13 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args
         const float dq = vx_f16_bits_to_f32(dh) * (float)ls;
         if (live && dq != 0.f) {
             const float dm = vx_f16_bits_to_f32(mh) * (float)lm;
+#pragma unroll
             for (int ii = 0; ii < 32; ++ii) {
                 int l = vx_nearest_int((x[ii] + dm) / dq);
                 L[ii] = (uint8_t)(l < 0 ? 0 : l > 15 ? 15 : l);
             }
+        } else {
+            vx_qkx2_levels(x, best, L);  // ggml keeps make_qkx2_quants' levels when d * sc == 0
         }
         // scales[12]: j < 4: sc[j] = ls_j | (ls_{j+4} >> 4) << 6,
         // sc[j+4] = lm_j | (lm_{j+4} >> 4) << 6; j >= 4: sc[j+4] = (ls_j & 15) | (lm_j & 15) << 4

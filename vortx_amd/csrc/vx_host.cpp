@@ -667,8 +667,14 @@ static int run_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, con
     a.nblk = out->cols / qk;
     a.x_vec = (a.xs_k == 1 && aligned16(cx.ptr) && a.xs_m % 4 == 0) ? 1u : 0u;
     DeviceGuard guard(ctx->device);
+    if (out->qtype == VX_Q4_K) {
+        // 32 super-blocks of the flattened (row, super-block) sequence per workgroup, grid-stride
+        uint64_t blocks = ((uint64_t)a.M * a.nblk + 31u) / 32u;
+        const uint64_t maxb = (uint64_t)ctx->num_cus * 64u;
+        if (blocks > maxb) blocks = maxb;
+        return launch(ctx, K_vx_quantize_q4_k, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    }
     const uint32_t gy = a.M < 65535u ? a.M : 65535u;
-    if (out->qtype == VX_Q4_K) return launch(ctx, K_vx_quantize_q4_k, dim3((a.nblk + 31u) / 32u, gy), dim3(256), 0, stream, a);
     return launch(ctx, out->qtype == VX_Q8_0 ? K_vx_quantize_q8_0 : K_vx_quantize_q4_0, dim3((a.nblk + 255u) / 256u, gy),
                   dim3(256), 0, stream, a);
 }
