@@ -45,7 +45,13 @@ typedef enum vx_status {
      * Maps to the reference's Err(GpuBackendError). */
     VX_ERR_HIP = 4,
     /* The embedded gfx950 code object failed to load (hipModuleLoadData). */
-    VX_ERR_NO_CODE_OBJECT = 5
+    VX_ERR_NO_CODE_OBJECT = 5,
+    /* A file could not be opened, sized or mapped (vortx_gguf.h). */
+    VX_ERR_IO = 6,
+    /* A file is not a well-formed GGUF file (vortx_gguf.h). */
+    VX_ERR_FORMAT = 7,
+    /* No tensor or metadata key of the requested name (vortx_gguf.h). */
+    VX_ERR_NOT_FOUND = 8
 } vx_status;
 
 /* ------------------------------------------------------------------ */

@@ -1,5 +1,5 @@
 """The C-ABI library on the CPU: it loads, exports every entry point that
-include/vortx_hip.h declares, and its host-side validation and routing
+include/*.h declare, and its host-side validation and routing
 behave without a GPU (no kernel is launched here)."""
 import ctypes as C
 import os
@@ -14,9 +14,13 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def _declared():
-    with open(os.path.join(ROOT, "include", "vortx_hip.h")) as f:
-        src = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
-    return sorted(set(re.findall(r"\b(vx_\w+)\s*\(", src)))
+    names = set()
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if h.endswith(".h"):
+            with open(os.path.join(ROOT, "include", h)) as f:
+                src = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+            names |= set(re.findall(r"\b(vx_\w+)\s*\(", src))
+    return sorted(names)
 
 
 def test_every_declared_symbol_is_exported():

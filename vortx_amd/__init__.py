@@ -9,7 +9,9 @@ Python-side mirror of the reference interface for this path:
 * :class:`QuantGemv` — block-quantized GEMV y = W x (Q8_0, Q4_0, Q4_K) and
   dequantize, which the reference does not have;
 * :class:`Contiguous` — ``Contiguous::launch`` (src/linalg/contiguous.rs:22-119),
-  the strided -> contiguous copy of 4-byte elements.
+  the strided -> contiguous copy of 4-byte elements;
+* :class:`GGUFFile` — GGUF model files (vortx_amd.gguf), which feed real
+  quantized weights to :class:`QuantGemv`.
 
 A view is either a torch tensor on the GPU (its sizes, strides and storage
 offset become the layout) or a ``(buffer, TensorLayout)`` pair, exactly like
@@ -26,7 +28,7 @@ from . import _ffi
 from ._ffi import (NONE_STRIDE, ROUTE_EMPTY, ROUTE_GEMV, ROUTE_NAIVE, ROUTE_TILED, VX_Q4_0, VX_Q4_K, VX_Q8_0,
                    VortxError, check, lib)
 
-__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "Contiguous", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
+__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "Contiguous", "GGUFFile", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
            "ROUTE_NAIVE", "ROUTE_TILED", "ROUTE_GEMV", "ROUTE_EMPTY", "qtype_info", "lib"]
 
 # Load eagerly: a missing library must fail at import, not at first call.
@@ -261,3 +263,6 @@ class Contiguous(_Context):
                 raise TypeError("offset must be a 4-byte integer tensor on the GPU")
             off = offset.data_ptr()
         check(lib().vx_contiguous(self._h, _stream(stream), C.byref(ov), C.byref(tv), off))
+
+
+from .gguf import GGUFFile  # noqa: E402  (needs QWeight and TensorLayout above)

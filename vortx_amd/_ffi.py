@@ -11,7 +11,8 @@ import os
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libvortx_hip.so")
 
-VX_OK, VX_ERR_SHAPE, VX_ERR_UNSUPPORTED, VX_ERR_INVALID, VX_ERR_HIP, VX_ERR_NO_CODE_OBJECT = range(6)
+(VX_OK, VX_ERR_SHAPE, VX_ERR_UNSUPPORTED, VX_ERR_INVALID, VX_ERR_HIP, VX_ERR_NO_CODE_OBJECT, VX_ERR_IO, VX_ERR_FORMAT,
+ VX_ERR_NOT_FOUND) = range(9)
 VX_Q4_0, VX_Q8_0, VX_Q4_K = 2, 8, 12
 ROUTE_NAIVE, ROUTE_TILED, ROUTE_GEMV, ROUTE_EMPTY = range(4)
 NONE_STRIDE = 0xFFFFFFFF
@@ -33,6 +34,23 @@ class VxMView(C.Structure):
 class VxQWeight(C.Structure):
     _fields_ = [("base", C.c_void_p), ("qtype", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
                 ("reserved", C.c_uint32), ("row_stride_bytes", C.c_uint64)]
+
+
+class VxGgufHeader(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("reserved", C.c_uint32), ("n_tensors", C.c_uint64), ("n_kv", C.c_uint64),
+                ("alignment", C.c_uint64), ("data_offset", C.c_uint64), ("data_size", C.c_uint64),
+                ("file_size", C.c_uint64)]
+
+
+class VxGgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("type", C.c_uint32), ("ne", C.c_uint64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64), ("size_known", C.c_uint32), ("reserved", C.c_uint32),
+                ("data", C.c_void_p)]
+
+
+class VxGgufKv(C.Structure):
+    _fields_ = [("key", C.c_char_p), ("type", C.c_uint32), ("elem_type", C.c_uint32), ("count", C.c_uint64),
+                ("data", C.c_void_p), ("nbytes", C.c_uint64)]
 
 
 # (name, restype, argtypes) for every exported entry point.
@@ -60,6 +78,18 @@ SIGNATURES = [
     ("vx_layout_narrow", C.c_int, [_P(VxLayout), C.c_uint32, C.c_uint32, C.c_uint32, _P(VxLayout)]),
     ("vx_layout_unsqueeze", C.c_int, [_P(VxLayout), C.c_uint32, _P(VxLayout)]),
     ("vx_layout_is_contiguous", C.c_int, [_P(VxLayout)]),
+    ("vx_gguf_open", C.c_int, [C.c_char_p, _P(C.c_void_p)]),
+    ("vx_gguf_close", C.c_int, [C.c_void_p]),
+    ("vx_gguf_get_header", C.c_int, [C.c_void_p, _P(VxGgufHeader)]),
+    ("vx_gguf_tensor_info", C.c_int, [C.c_void_p, C.c_uint64, _P(VxGgufTensor)]),
+    ("vx_gguf_find_tensor", C.c_int, [C.c_void_p, C.c_char_p, _P(C.c_uint64)]),
+    ("vx_gguf_kv_info", C.c_int, [C.c_void_p, C.c_uint64, _P(VxGgufKv)]),
+    ("vx_gguf_find_key", C.c_int, [C.c_void_p, C.c_char_p, _P(C.c_uint64)]),
+    ("vx_gguf_kv_string", C.c_int, [C.c_void_p, C.c_uint64, C.c_uint64, _P(C.c_void_p), _P(C.c_uint64)]),
+    ("vx_gguf_type_size", C.c_int, [C.c_uint32, _P(C.c_uint32), _P(C.c_uint32)]),
+    ("vx_gguf_upload", C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p]),
+    ("vx_gguf_qweight", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, _P(VxQWeight)]),
+    ("vx_gguf_view", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, _P(VxCView)]),
     ("vx_status_string", C.c_char_p, [C.c_int]),
     ("vx_last_error_message", C.c_char_p, []),
     ("vx_last_hip_error", C.c_int, []),
@@ -98,4 +128,4 @@ class VortxError(RuntimeError):
 
 def check(status: int) -> None:
     if status != VX_OK:
-        raise VortxError(status, lib().vx_last_error_message().decode())
+        raise VortxError(status, lib().vx_last_error_message().decode("utf-8", errors="replace"))

@@ -49,7 +49,7 @@ int fail_hip(int hip_error, const char* what) {
     return VX_ERR_HIP;
 }
 
-static void clear_error() {
+void clear_error() {
     t_msg.clear();
     t_hip = 0;
 }
@@ -833,6 +833,9 @@ const char* vx_status_string(int status) {
     case VX_ERR_INVALID: return "VX_ERR_INVALID";
     case VX_ERR_HIP: return "VX_ERR_HIP";
     case VX_ERR_NO_CODE_OBJECT: return "VX_ERR_NO_CODE_OBJECT";
+    case VX_ERR_IO: return "VX_ERR_IO";
+    case VX_ERR_FORMAT: return "VX_ERR_FORMAT";
+    case VX_ERR_NOT_FOUND: return "VX_ERR_NOT_FOUND";
     default: return "VX_ERR_UNKNOWN";
     }
 }

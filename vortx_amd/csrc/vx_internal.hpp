@@ -12,6 +12,8 @@ namespace vx {
 // Records `msg` as this thread's last error and returns `status`.
 int fail(int status, const char* msg);
 int fail_hip(int hip_error, const char* what);
+// Clears this thread's last error (every entry point starts with it).
+void clear_error();
 
 int layout_contiguous(const uint32_t* size, uint32_t rank, vx_layout* out);
 int layout_canonicalize(const vx_layout* in, vx_layout* out);
