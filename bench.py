@@ -8,9 +8,11 @@ cannot serve them), inputs resident in HBM before timing starts.
 
 Secondary lines in the same JSON object: the other BASELINE GEMV configs
 (Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 b=1, Q4_0 11008 x 4096
-b=8, Q4_K 14336 x 4096 b=16; GB/s of algorithmic bytes) and the f32 GEMM
-4096^3 (TFLOP/s), each with its roofline, plus CPU baselines from the
-oracle's OpenMP restatements on the host cores.
+b=8, Q4_K 14336 x 4096 b=16; GB/s of algorithmic bytes), the contiguous
+copy of a transposed 8192^2 view, the Q8_0 and Q4_K quantizers on
+14336 x 4096, the GGUF file -> HBM upload (against the PCIe 5.0 x16 link)
+and the f32 GEMM 4096^3 (TFLOP/s), each with its roofline, plus CPU
+baselines from the oracle's OpenMP restatements on the host cores.
 
 Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
 (captured eager launches) between two synchronizations (wall clock).
@@ -35,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, public spec
 F32_MFMA_PEAK_TFS = 157.3   # MI355X dense f32 matrix, public spec
+PCIE_PEAK_GBS = 64.0        # host link: PCIe 5.0 x16, one direction
 METRIC = "Q4_0/Q8_0 GEMV HBM GB/s at 11008x4096 b=1; f32 GEMM TFLOP/s at 4096^3"
 
 
@@ -206,6 +209,47 @@ def time_quantize(qtype: int, M: int, K: int, steps: int, warmup: int):
             "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
 
 
+def time_gguf_upload(steps: int):
+    """GGUF model file -> HBM (vx_gguf_upload) for a 1.14 GB file of four Q8_0
+    65536x4096 tensors: parse, then the data section into a device buffer
+    that was written once before (a fresh allocation's first write measures
+    the device's page mapping, not the loader). The file sits in the page
+    cache, as right after a download or a previous load."""
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    import vortx_amd as vx
+    from tests import gguf_writer as W
+
+    K, M = 4096, 65536
+    blob = np.random.default_rng(0).integers(0, 256, M * (K // 32) * 34, dtype=np.uint8).tobytes()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "bench.gguf")
+        with open(path, "wb") as fh:
+            fh.write(W.build([("general.architecture", W.STRING, "llama")],
+                             [(f"blk.{i}.ffn_up.weight", [K, M], 8, blob) for i in range(4)]))
+        del blob
+        t0 = time.perf_counter()
+        f = vx.GGUFFile(path)
+        open_ms = (time.perf_counter() - t0) * 1e3
+        n = f.header["data_size"]
+        ctx = vx.QuantGemv(0)
+        buf = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+        f.upload(ctx, buf)
+        times = []
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            f.upload(ctx, buf)
+            times.append(time.perf_counter() - t0)
+        f.close()
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": n / med / 1e9, "bytes": n, "ms_per_step": med * 1e3, "open_ms": open_ms}
+
+
 def cpu_baselines(threads: int):
     """Oracle OpenMP restatements on the host cores (bounded samples)."""
     import numpy as np
@@ -284,6 +328,9 @@ def main() -> int:
         log(f"[quantize_{label}] {r}")
         quant.append((label, r))
 
+    gg = time_gguf_upload(5)
+    log(f"[gguf_upload] {gg}")
+
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     cpu = None if args.no_cpu else cpu_baselines(threads)
     if cpu:
@@ -327,6 +374,11 @@ def main() -> int:
              **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block"}
                 if label == "q4_k" else {})}
             for label, r in quant
+        ] + [
+            {"workload": "GGUF file (page cache) -> HBM upload, 1.14 GB data section (vx_gguf_upload)",
+             "value": gg["value"], "unit": "GB/s", "ms_per_step": gg["ms_per_step"], "open_ms": gg["open_ms"],
+             "roofline": {"bound": "pcie", "achieved": gg["value"], "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+                          "frac": gg["value"] / PCIE_PEAK_GBS, "traffic": None}},
         ] + [
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
