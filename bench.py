@@ -150,6 +150,37 @@ def time_gemm(M: int, N: int, K: int, steps: int, warmup: int):
             "ms_per_step": wall * 1e3 / steps}
 
 
+def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int):
+    """vx_gemm_f32_ex: out[b] = A[b] W + 1.0 * out[b] for a batch of B
+    activations A [B, M, K] sharing one W [K, N] (broadcast batch dim) with
+    the beta = 1 epilogue (C read and written): 2 B M N K flops."""
+    import torch
+
+    import vortx_amd as vx
+    from vortx_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    a = S.uniform((B, M, K), 3, dev)
+    w = S.uniform((K, N), 4, dev)
+    c = torch.zeros((B, M, N), device=dev)
+    gm = vx.Gemm(0)
+    for _ in range(warmup):
+        gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    stream = torch.cuda.current_stream()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    flops = 2.0 * B * M * N * K
+    return {"value": flops * steps / wall / 1e12, "avg_launch_ms": e0.elapsed_time(e1) / steps, "flops": flops,
+            "ms_per_step": wall * 1e3 / steps}
+
+
 def time_contiguous(shape, steps: int, warmup: int):
     """vortx's Contiguous op (src/linalg/contiguous.rs) on a transposed f32
     view: bytes = 8 per element (read + write); 4 rotating 256 MB sources."""
@@ -320,6 +351,8 @@ def main() -> int:
     gsteps = max(5, min(50, args.steps // 40))
     gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm] {gemm}")
+    gemm_b = time_gemm_broadcast(8, 1024, 4096, 4096, gsteps, max(2, args.warmup // 100))
+    log(f"[gemm_broadcast] {gemm_b}")
     cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
     log(f"[contiguous] {cont}")
     quant = []
@@ -342,6 +375,7 @@ def main() -> int:
                 "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(name)}
 
     gemm_ach = gemm["flops"] / (gemm["avg_launch_ms"] * 1e-3) / 1e12
+    gemm_b_ach = gemm_b["flops"] / (gemm_b["avg_launch_ms"] * 1e-3) / 1e12
     line = {
         "metric": METRIC,
         "value": q40["value"],
@@ -385,6 +419,11 @@ def main() -> int:
              "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
                           "frac": gemm_ach / F32_MFMA_PEAK_TFS, "traffic": load_traffic("gemm_f32_4096")},
              "cpu_baseline": cpu["gemm1024"] if cpu else None},
+            {"workload": "broadcast f32 GEMM out[b] = A[b] W + out[b], A [8, 1024, 4096], shared W [4096, 4096] "
+                         "(vx_gemm_f32_ex, beta = 1)", "value": gemm_b["value"], "unit": "TFLOP/s",
+             "ms_per_step": gemm_b["ms_per_step"],
+             "roofline": {"bound": "mfma", "achieved": gemm_b_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                          "frac": gemm_b_ach / F32_MFMA_PEAK_TFS, "traffic": load_traffic("gemm_f32_broadcast_8x1024")}},
         ],
     }
     print(json.dumps(line), flush=True)

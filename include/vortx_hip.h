@@ -145,6 +145,33 @@ int vx_gemm_f32_naive(vx_ctx ctx, vx_stream stream, const vx_mview* out,
 int vx_gemm_f32_tiled(vx_ctx ctx, vx_stream stream, const vx_mview* out,
                       const vx_cview* lhs, const vx_cview* rhs);
 
+/* Options of vx_gemm_f32_ex. */
+typedef enum vx_gemm_flags {
+    /* Batch dims broadcast: after canonicalization (rank 4, leading 1s),
+     * each of lhs's and rhs's dims 0 and 1 may be 1 where out's is larger;
+     * that operand is then reused along the dim (stride 0), the semantics
+     * of TensorLayout::broadcast (src/shapes.rs:346-391) that the reference
+     * leaves as a TODO in Gemm::dispatch (src/linalg/gemm.rs:64). */
+    VX_GEMM_BROADCAST = 1
+} vx_gemm_flags;
+
+typedef struct vx_gemm_opts {
+    float alpha;       /* out = alpha * (lhs x rhs) + beta * out */
+    float beta;        /* 0: out is only written (NaN / inf in out do not propagate) */
+    uint32_t flags;    /* bitwise OR of vx_gemm_flags */
+    uint32_t reserved; /* must be 0 */
+} vx_gemm_opts;
+
+/* Gemm::dispatch with an alpha / beta epilogue and optional batch
+ * broadcasting (no reference counterpart: the reference's out is only
+ * written, :70-104 require equal batch dims). Same routes and kernels as
+ * vx_gemm_f32; opts == NULL means alpha 1, beta 0, no flags, which is
+ * vx_gemm_f32. out must not overlap itself (a dim of size > 1 with stride
+ * 0 is VX_ERR_INVALID). With beta != 0 each output element is read once
+ * before it is written. */
+int vx_gemm_f32_ex(vx_ctx ctx, vx_stream stream, const vx_mview* out,
+                   const vx_cview* lhs, const vx_cview* rhs, const vx_gemm_opts* opts);
+
 /* Kernel route vx_gemm_f32 takes for these views, without launching
  * (host logic only; usable without a GPU). */
 typedef enum vx_gemm_route {

@@ -177,6 +177,15 @@ class Gemm(_Context):
     def dispatch(self, out, lhs, rhs, stream=None) -> None:
         self._call(lib().vx_gemm_f32, out, lhs, rhs, stream)
 
+    def dispatch_ex(self, out, lhs, rhs, alpha: float = 1.0, beta: float = 0.0, broadcast: bool = False,
+                    stream=None) -> None:
+        """out = alpha * (lhs x rhs) + beta * out (vx_gemm_f32_ex); out is not
+        read when beta == 0. ``broadcast``: batch dims of lhs / rhs of size 1
+        are reused along out's (src/shapes.rs:346-391 semantics)."""
+        o, l, r = _view_of(out, True), _view_of(lhs, False), _view_of(rhs, False)
+        opts = _ffi.VxGemmOpts(alpha, beta, _ffi.VX_GEMM_BROADCAST if broadcast else 0, 0)
+        check(lib().vx_gemm_f32_ex(self._h, _stream(stream), C.byref(o), C.byref(l), C.byref(r), C.byref(opts)))
+
     def dispatch_naive(self, out, lhs, rhs, stream=None) -> None:
         self._call(lib().vx_gemm_f32_naive, out, lhs, rhs, stream)
 

@@ -36,6 +36,13 @@ class VxQWeight(C.Structure):
                 ("reserved", C.c_uint32), ("row_stride_bytes", C.c_uint64)]
 
 
+class VxGemmOpts(C.Structure):
+    _fields_ = [("alpha", C.c_float), ("beta", C.c_float), ("flags", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+VX_GEMM_BROADCAST = 1
+
+
 class VxGgufHeader(C.Structure):
     _fields_ = [("version", C.c_uint32), ("reserved", C.c_uint32), ("n_tensors", C.c_uint64), ("n_kv", C.c_uint64),
                 ("alignment", C.c_uint64), ("data_offset", C.c_uint64), ("data_size", C.c_uint64),
@@ -62,6 +69,7 @@ SIGNATURES = [
     ("vx_gemm_f32", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
     ("vx_gemm_f32_naive", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
     ("vx_gemm_f32_tiled", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView)]),
+    ("vx_gemm_f32_ex", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), _P(VxCView), _P(VxGemmOpts)]),
     ("vx_gemm_f32_route", C.c_int, [_P(VxMView), _P(VxCView), _P(VxCView), _P(C.c_int)]),
     ("vx_gemv_q", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView)]),
     ("vx_gemv_q_ex", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView), C.c_uint32]),

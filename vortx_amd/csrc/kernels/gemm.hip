@@ -33,6 +33,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 #define MODE_XC 1  // contiguous along M (for A) / N (for B), 16-byte aligned
 #define MODE_GEN 2 // anything else: scalar loads
 
+// Output epilogue: alpha * acc + beta * c, where c is read only when
+// beta != 0 (the BLAS convention: out may hold NaN when beta == 0). With
+// alpha == 1 and beta == 0 the result is acc itself.
+__device__ __forceinline__ void vx_epilogue(float* c, float acc, float alpha, float beta) {
+    *c = beta == 0.f ? alpha * acc : alpha * acc + beta * *c;
+}
+
 // ---------------------------------------------------------------- naive
 extern "C" __global__ __launch_bounds__(64) void vx_gemm_naive(vx_gemm_args p) {
     const uint32_t j = blockIdx.x * 64u + threadIdx.x;
@@ -48,7 +55,12 @@ extern "C" __global__ __launch_bounds__(64) void vx_gemm_naive(vx_gemm_args p) {
 #pragma clang fp contract(off)
         sum = sum + a[(int64_t)k * p.as[3]] * b[(int64_t)k * p.bs[2]];
     }
-    p.c[bn * p.cs[0] + bc * p.cs[1] + (int64_t)i * p.cs[2] + (int64_t)j * p.cs[3]] = sum;
+    float* c = p.c + bn * p.cs[0] + bc * p.cs[1] + (int64_t)i * p.cs[2] + (int64_t)j * p.cs[3];
+    {
+        // the epilogue rounds after each operation too: (alpha * sum) + (beta * c)
+#pragma clang fp contract(off)
+        *c = p.beta == 0.f ? p.alpha * sum : p.alpha * sum + p.beta * *c;
+    }
 }
 
 // ----------------------------------------------------------------- mfma
@@ -216,7 +228,8 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t row = m0 + wm * 64u + 32u * i + 8u * (v >> 2) + 4u * lk + (v & 3);
-                if (row < p.M && col < p.N) Cp[(int64_t)row * p.cs[2] + (int64_t)col * p.cs[3]] = acc[i][j][v];
+                if (row < p.M && col < p.N)
+                    vx_epilogue(Cp + (int64_t)row * p.cs[2] + (int64_t)col * p.cs[3], acc[i][j][v], p.alpha, p.beta);
             }
         }
 }
@@ -268,5 +281,5 @@ extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_f32(vx_gemv_f32_args
     for (uint32_t k = K4 + lane; k < p.K; k += 64u) acc = __builtin_fmaf(a[k], x[(int64_t)k * p.xs_k], acc);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (lane == 0) p.y[bn * p.y_bs[0] + bc * p.y_bs[1] + (int64_t)row * p.ys_m] = acc;
+    if (lane == 0) vx_epilogue(p.y + bn * p.y_bs[0] + bc * p.y_bs[1] + (int64_t)row * p.ys_m, acc, p.alpha, p.beta);
 }

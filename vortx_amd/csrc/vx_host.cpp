@@ -217,14 +217,24 @@ struct GemmPlan {
 };
 
 // Canonicalize and validate exactly like Gemm::dispatch
-// (src/linalg/gemm.rs:66-104), then choose the route (:111-118).
-static int plan_gemm(const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs, int force, GemmPlan* p) {
+// (src/linalg/gemm.rs:66-104), then choose the route (:111-118). With
+// `broadcast`, a batch dim (0 or 1) of lhs or rhs may instead be 1 where
+// out's is larger: its stride becomes 0, as TensorLayout::broadcast
+// (src/shapes.rs:346-391) sets it, so the kernels reuse that operand.
+static int plan_gemm(const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs, int force, GemmPlan* p,
+                     bool broadcast = false) {
     if (!out || !lhs || !rhs) return fail(VX_ERR_INVALID, "null view");
     int s;
     if ((s = canon_view(out->base, &out->layout, &p->o, "out"))) return s;
     if ((s = canon_view(lhs->base, &lhs->layout, &p->l, "lhs"))) return s;
     if ((s = canon_view(rhs->base, &rhs->layout, &p->r, "rhs"))) return s;
-    const vx_layout &so = p->o.l, &sl = p->l.l, &sr = p->r.l;
+    vx_layout &so = p->o.l, &sl = p->l.l, &sr = p->r.l;
+    if (broadcast) {
+        for (int d = 0; d < 2; ++d) {
+            if (sl.size[d] == 1 && so.size[d] != 1) sl.size[d] = so.size[d], sl.stride[d] = 0;
+            if (sr.size[d] == 1 && so.size[d] != 1) sr.size[d] = so.size[d], sr.stride[d] = 0;
+        }
+    }
     const bool ok = so.size[0] == sl.size[0] && so.size[1] == sl.size[1] && sl.size[0] == sr.size[0] &&
                     sl.size[1] == sr.size[1] && so.size[2] == sl.size[2] && so.size[3] == sr.size[3] &&
                     sl.size[3] == sr.size[2];
@@ -271,12 +281,28 @@ static int operand_mode(const Canon& c, int kdim, int xdim, uint32_t nb, uint32_
 }
 
 static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs,
-                    int force) {
+                    int force, const vx_gemm_opts* opts = nullptr) {
     clear_error();
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    float alpha = 1.f, beta = 0.f;
+    bool broadcast = false;
+    if (opts) {
+        if (opts->reserved != 0 || (opts->flags & ~(uint32_t)VX_GEMM_BROADCAST))
+            return fail(VX_ERR_INVALID, "unknown gemm option flags (reserved must be 0)");
+        alpha = opts->alpha;
+        beta = opts->beta;
+        broadcast = (opts->flags & VX_GEMM_BROADCAST) != 0;
+    }
     GemmPlan p;
-    int s = plan_gemm(out, lhs, rhs, force, &p);
+    int s = plan_gemm(out, lhs, rhs, force, &p, broadcast);
     if (s) return s;
+    if (opts) {
+        // every output element must have its own address: the epilogue reads it, and
+        // different (i, j) writing one address would race
+        for (int d = 0; d < 4; ++d)
+            if (p.o.l.size[d] > 1 && p.o.l.stride[d] == 0)
+                return fail(VX_ERR_INVALID, "out has a zero stride on a dimension of size > 1");
+    }
     if (p.route == VX_ROUTE_EMPTY) return VX_OK;
     DeviceGuard guard(ctx->device);
     const uint32_t batch = p.nb * p.nc;
@@ -298,6 +324,8 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
         g.x_bs[1] = p.r.l.stride[1];
         g.y_bs[0] = p.o.l.stride[0];
         g.y_bs[1] = p.o.l.stride[1];
+        g.alpha = alpha;
+        g.beta = beta;
         return launch(ctx, K_vx_gemv_f32, dim3((p.M + 3) / 4, batch, 1), dim3(VX_WG), 0, stream, g);
     }
     vx_gemm_args a{};
@@ -313,6 +341,8 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
     a.M = p.M;
     a.N = p.N;
     a.K = p.K;
+    a.alpha = alpha;
+    a.beta = beta;
     if (p.route == VX_ROUTE_NAIVE) {
         return launch(ctx, K_vx_gemm_naive, dim3((p.N + 63) / 64, p.M, batch), dim3(64), 0, stream, a);
     }
@@ -735,6 +765,11 @@ int vx_device_info(vx_ctx ctx, int* device, int* num_cus) {
 
 int vx_gemm_f32(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs) {
     return vx::run_gemm(ctx, stream, out, lhs, rhs, vx::FORCE_AUTO);
+}
+
+int vx_gemm_f32_ex(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs,
+                   const vx_gemm_opts* opts) {
+    return vx::run_gemm(ctx, stream, out, lhs, rhs, vx::FORCE_AUTO, opts);
 }
 
 int vx_gemm_f32_naive(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_cview* lhs, const vx_cview* rhs) {

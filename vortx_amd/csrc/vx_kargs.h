@@ -25,7 +25,7 @@ typedef struct vx_gemm_args {
     uint32_t batch_c;  /* size of dim 1; grid z = n * batch_c */
     uint32_t M, N, K;
     uint32_t tiles_m, tiles_n;
-    uint32_t pad0, pad1;
+    float alpha, beta;  /* c = alpha * acc + beta * c (c not read when beta == 0) */
 } vx_gemm_args;
 
 /* Block-quantized GEMV / dequantize. */
@@ -54,6 +54,7 @@ typedef struct vx_gemv_f32_args {
     int64_t ys_m;
     uint32_t M, K;
     uint32_t batch_c;
+    float alpha, beta;  /* y = alpha * acc + beta * y (y not read when beta == 0) */
     uint32_t pad0;
     int64_t a_bs[2], x_bs[2], y_bs[2]; /* batch strides (dims n, c) */
 } vx_gemv_f32_args;
