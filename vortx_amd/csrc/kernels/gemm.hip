@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_dpp.hpp"
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -279,7 +280,6 @@ extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_f32(vx_gemv_f32_args
         }
     }
     for (uint32_t k = K4 + lane; k < p.K; k += 64u) acc = __builtin_fmaf(a[k], x[(int64_t)k * p.xs_k], acc);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    acc = vx_wave_sum(acc);
     if (lane == 0) vx_epilogue(p.y + bn * p.y_bs[0] + bc * p.y_bs[1] + (int64_t)row * p.ys_m, acc, p.alpha, p.beta);
 }

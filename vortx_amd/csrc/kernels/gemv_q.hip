@@ -178,7 +178,10 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
     // and the wait counts stay exact
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t nwv = gridDim.x * (WGT / 64u);
-    const uint32_t gw = blockIdx.x * (WGT / 64u) + wave;
+    // waves interleaved over the CUs (wave-major), so the rows left over
+    // after whole rounds of nwv spread evenly: at M = 11008 every CU gets 43
+    // rows (CU-major numbering gives 176 CUs 48 rows and 80 CUs 32)
+    const uint32_t gw = wave * gridDim.x + blockIdx.x;
     const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
     const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
     const uint32_t nitems = nrows * npass;
@@ -206,11 +209,15 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
     // 2. the first item (clamped: past the end an item repeats the last
     //    one, which the cache serves; y is written only for real rows).
     const uint8_t* wbase = a.w;
+    // Past the last item the ring still issues its loads (so that every
+    // round issues the same loads and the wait counts stay exact), but all
+    // lanes then read unit 0 of the last item's row: one cache line the
+    // wave has just fetched, so the wave does not end waiting on a full row.
     auto item_ptr = [&](uint32_t it, uint32_t& unit) {
         const uint32_t c = nitems ? min(it, nitems - 1u) : 0u;
         const uint32_t ri = c / npass, p = c - ri * npass;
         const uint32_t row = min(gw + ri * nwv, a.M - 1u);
-        unit = min(64u * p + lane, nunits - 1u);
+        unit = it < nitems ? min(64u * p + lane, nunits - 1u) : 0u;
         return wbase + (uint64_t)row * a.row_stride;
     };
     uint32_t wr[P][NW];
@@ -227,10 +234,7 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
         if ((uint32_t)i * WGT >= total) break;
         const uint32_t f = t + WGT * (uint32_t)i;
         const bool in = f < total;
-        float ps = in ? (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w) : 0.f;
-        ps += __shfl_xor(ps, 1, 64);
-        ps += __shfl_xor(ps, 2, 64);
-        ps += __shfl_xor(ps, 4, 64);
+        const float ps = vx_sum8(in ? (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w) : 0.f);
         if (in) {
             vx_lds_x[(f & 15u) * upitch + (f >> 4)] = xr[i];
             if ((f & 7u) == 0u) sxs[2u * (f >> 4) + ((f >> 3) & 1u)] = ps;

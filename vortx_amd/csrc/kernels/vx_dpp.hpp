@@ -1,0 +1,39 @@
+// vx_dpp.hpp — wave64 reductions on DPP lane moves (gfx950).
+//
+// __shfl_xor lowers to ds_bpermute, a round trip through the LDS crossbar
+// per step; a six-step wave sum built from it sits on a wave's critical
+// path for ~700 cycles. DPP moves are VALU operand modifiers: the same sum
+// takes six dependent VALU adds.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+// DPP controls used here (GFX9 encoding):
+//   0xB1  quad_perm [1,0,3,2]   lane i <- i ^ 1
+//   0x4E  quad_perm [2,3,0,1]   lane i <- i ^ 2
+//   0x141 row_half_mirror       lane i <- 7 - i   within each 8 lanes
+//   0x140 row_mirror            lane i <- 15 - i  within each 16 lanes
+//   0x142 row_bcast:15          row r <- lane 15 of row r - 1
+//   0x143 row_bcast:31          rows 2, 3 <- lane 31
+// ROWS masks the 16-lane rows that are written; the others (and any lane
+// whose source is invalid) receive 0, so v + vx_dpp(v) leaves them as v.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float vx_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false));
+}
+
+// Sum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float vx_sum8(float v) {
+    v += vx_dpp<0xB1>(v);
+    v += vx_dpp<0x4E>(v);
+    return v + vx_dpp<0x141>(v);
+}
+
+// Sum over the 64 lanes, returned in every lane (wave-uniform).
+__device__ __forceinline__ float vx_wave_sum(float v) {
+    v = vx_sum8(v);
+    v += vx_dpp<0x140>(v);       // each row of 16 holds its row sum
+    v += vx_dpp<0x142, 0xA>(v);  // rows 1, 3 += rows 0, 2
+    v += vx_dpp<0x143, 0xC>(v);  // rows 2, 3 += lane 31 (rows 0 + 1): lane 63 has the total
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}

@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_dpp.hpp"
 
 #define VX_Q4_0 2
 #define VX_Q8_0 8
@@ -327,12 +328,6 @@ __device__ __forceinline__ void vx_decode32(const uint8_t* row, uint32_t kb, flo
             o[l] = __fsub_rn(__fmul_rn(ds, (float)q), mm);
         }
     }
-}
-
-__device__ __forceinline__ float vx_wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
 }
 
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
