@@ -779,13 +779,8 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     // 2. split x into two int8 levels per 32-block (8 float4 = 8 lanes).
     auto split = [&](uint32_t f, f32x4 v, bool in) {
         if (!in) v = f32x4{0.f, 0.f, 0.f, 0.f};
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        float ps = (v.x + v.y) + (v.z + v.w);
-#pragma unroll
-        for (int sft = 1; sft < 8; sft <<= 1) {
-            m = fmaxf(m, __shfl_xor(m, sft, 64));
-            ps += __shfl_xor(ps, sft, 64);
-        }
+        const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float ps = vx_sum8((v.x + v.y) + (v.z + v.w));
         const bool fin = m < __builtin_inff();
         const float c1 = m * (1.f / 126.f), c2 = c1 * (1.f / 254.f);
         const float i1 = (fin && m > 0.f) ? 126.f / m : 0.f, i2 = i1 * 254.f;

@@ -29,6 +29,13 @@ __device__ __forceinline__ float vx_sum8(float v) {
     return v + vx_dpp<0x141>(v);
 }
 
+// Maximum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float vx_max8(float v) {
+    v = fmaxf(v, vx_dpp<0xB1>(v));
+    v = fmaxf(v, vx_dpp<0x4E>(v));
+    return fmaxf(v, vx_dpp<0x141>(v));
+}
+
 // Sum over the 64 lanes, returned in every lane (wave-uniform).
 __device__ __forceinline__ float vx_wave_sum(float v) {
     v = vx_sum8(v);
