@@ -894,8 +894,7 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
             // row j's sums over the four units of this wave's rounds
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
-                float v = acc[c] + __shfl_xor(acc[c], 16, 64);
-                v += __shfl_xor(v, 32, 64);
+                const float v = vx_sum_rows4(acc[c]);
                 if ((uint32_t)c < B && lane < 16u) red[((ts * 16u + wave) * B + c) * 16u + lane] = v;
                 acc[c] = 0.f;
             }

@@ -44,3 +44,29 @@ __device__ __forceinline__ float vx_wave_sum(float v) {
     v += vx_dpp<0x143, 0xC>(v);  // rows 2, 3 += lane 31 (rows 0 + 1): lane 63 has the total
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
+// Sum over the four 16-lane rows: lane l gets v[l % 16] + v[l % 16 + 16] +
+// v[l % 16 + 32] + v[l % 16 + 48], added as (row 0 + row 1) + (row 2 + row 3).
+// v_permlane16_swap exchanges odd rows of its first operand with even rows
+// of its second, v_permlane32_swap the upper half of the first with the
+// lower half of the second (gfx950 VALU ops); with both operands v, the two
+// results of each swap add up to the pairwise row sums in every lane.
+// Both operands and both results pass through empty asm: this compiler
+// otherwise folds the two results of a swap into one (a[0] + a[1] came out
+// as a[0] + a[0]), and the swap needs its operands in two registers.
+__device__ __forceinline__ void vx_pin2(unsigned& x, unsigned& y) { asm volatile("" : "+v"(x), "+v"(y)); }
+
+__device__ __forceinline__ float vx_sum_rows4(float v) {
+    unsigned u = __builtin_bit_cast(unsigned, v), u2 = u;
+    vx_pin2(u, u2);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u2, false, false);
+    unsigned a0 = a[0], a1 = a[1];
+    vx_pin2(a0, a1);
+    const float p = __builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a1);
+    unsigned w = __builtin_bit_cast(unsigned, p), w2 = w;
+    vx_pin2(w, w2);
+    const auto b = __builtin_amdgcn_permlane32_swap(w, w2, false, false);
+    unsigned b0 = b[0], b1 = b[1];
+    vx_pin2(b0, b1);
+    return __builtin_bit_cast(float, b0) + __builtin_bit_cast(float, b1);
+}
