@@ -196,15 +196,16 @@ int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 
 /* vx_gemv_q with options; flags is a bitwise OR of vx_gemv_flags.
- * Batch 1 (B == 1) multiplies the exactly decoded weights with f32 x (f32
- * FMA accumulation) by default. Batches (B >= 2) run on the int8 matrix
- * cores: each 32-element block of each column of x is split into two int8
- * levels with one f32 scale, x ~= c (254 x1 + x2), |error| <= c/2 ~
- * 1.6e-5 max|x_block|; products and block sums are exact in int32 and the
- * scaling is f32. VX_GEMV_X_INT8 applies the same split to batch-1 launches
- * (reduced with v_dot4_i32_i8). The environment variable
- * VX_GEMV_BATCHED=simt selects exact-f32 batch kernels instead. */
-typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1 } vx_gemv_flags;
+ * By default x is split, per 32-element block of each column, into two
+ * int8 levels with one f32 scale, x ~= c (254 x1 + x2), |error| <= c/2 ~
+ * 1.6e-5 max|x_block|; products and block sums with the exactly decoded
+ * weights are exact in int32 and the scaling is f32. Batch 1 reduces with
+ * v_dot4_i32_i8, batches (B >= 2) on the int8 matrix cores. VX_GEMV_X_F32
+ * keeps x in f32 instead (f32 FMA on the exactly decoded weights; slower);
+ * VX_GEMV_X_INT8 names the default split and may not be combined with it.
+ * The environment variable VX_GEMV_BATCHED=simt selects the exact-f32
+ * kernels for batches only. */
+typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1, VX_GEMV_X_F32 = 2 } vx_gemv_flags;
 int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_cview* x, uint32_t flags);
 

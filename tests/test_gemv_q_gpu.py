@@ -65,13 +65,13 @@ def test_dequantize_strided_output(qgemv, qtype):
     assert torch.isnan(big[:, 0::2]).all(), "wrote outside the view"
 
 
-def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False):
+def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False, x_f32=False):
     w = S.quant_weights(qtype, M, K, seed=seed, device=DEV)
     x = S.activations(B, K, seed=seed + 1, device=DEV)
     y = torch.full((B, M), float("nan"), device=DEV) if y_out is None else y_out
     xv = x.t() if x_kb is None else x_kb(x)
     yv = y.t() if y_out is None else y
-    qgemv.dispatch(yv, vx.QWeight(w, qtype, M, K), xv, x_int8=x_int8)
+    qgemv.dispatch(yv, vx.QWeight(w, qtype, M, K), xv, x_int8=x_int8, x_f32=x_f32)
     torch.cuda.synchronize()
     ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
     return yv.cpu().numpy(), ref
@@ -104,9 +104,10 @@ def test_gemv_parity_configs(qgemv, qtype, M, K, B):
     got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=7)
     assert_close(got, ref, what=f"{QN[qtype]} {M}x{K} b{B}")
     if B == 1:
-        note(f"gemv config int8-x {QN[qtype]} {M}x{K}")
-        got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=8, x_int8=True)
-        assert_close(got, ref, what=f"int8-x {QN[qtype]} {M}x{K}")
+        # the exact-f32 batch-1 kernel: f32 accumulation only, so 1e-5 holds
+        note(f"gemv config f32-x {QN[qtype]} {M}x{K}")
+        got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=8, x_f32=True)
+        assert_close(got, ref, tol=1e-5, what=f"f32-x {QN[qtype]} {M}x{K}")
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
@@ -121,8 +122,9 @@ def test_gemv_int8x_path_small(qgemv, qtype, M, K):
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 def test_gemv_x_edge_values(qgemv, qtype):
-    """Both batch-1 paths with x blocks that are all zero, tiny, huge, or one
-    large outlier among small values; K spanning several LDS chunks."""
+    """Both batch-1 x modes (int8 levels, f32) with x blocks that are all
+    zero, tiny, huge, or one large outlier among small values; K spanning
+    several LDS chunks (the per-row-group kernels)."""
     M, K = 40, 64 * 300
     note(f"gemv i8 edge x {QN[qtype]}")
     w = S.quant_weights(qtype, M, K, seed=3, device=DEV)
@@ -134,11 +136,11 @@ def test_gemv_x_edge_values(qgemv, qtype):
     x[0, 100] = 50.0
     y = torch.full((M,), float("nan"), device=DEV)
     ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())[:, 0]
-    for x_int8 in (False, True):
+    for x_f32 in (False, True):
         y.fill_(float("nan"))
-        qgemv.dispatch(y, vx.QWeight(w, qtype, M, K), x[0], x_int8=x_int8)
+        qgemv.dispatch(y, vx.QWeight(w, qtype, M, K), x[0], x_f32=x_f32)
         torch.cuda.synchronize()
-        assert_close(y.cpu().numpy(), ref, what=f"x_int8={x_int8}")
+        assert_close(y.cpu().numpy(), ref, what=f"x_f32={x_f32}")
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
@@ -168,27 +170,43 @@ def test_gemv_batched_x_edge_values(qgemv, qtype, B):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
-@pytest.mark.parametrize("path", ["simt", "rows"])
+@pytest.mark.parametrize("path", ["simt", "f32", "rows", "rows-f32"])
 def test_gemv_alternate_kernels(qgemv, qtype, path, monkeypatch):
-    """The exact-f32 batched kernels (VX_GEMV_BATCHED=simt) and the
-    per-row-group batch-1 kernel (VX_GEMV_B1=rows) stay selectable."""
+    """The exact-f32 kernels (VX_GEMV_X_F32 at every batch size, or
+    VX_GEMV_BATCHED=simt for batches) and the per-row-group batch-1 kernels
+    (VX_GEMV_B1=rows, int8 or f32 x) stay selectable. The f32-x kernels
+    accumulate in f32 only and are held to 1e-5."""
     M, K = 131, 4096
+    x_f32 = path in ("f32", "rows-f32")
     if path == "simt":
         monkeypatch.setenv("VX_GEMV_BATCHED", "simt")
-        Bs = [2, 4, 8, 16]
-    else:
+    if path.startswith("rows"):
         monkeypatch.setenv("VX_GEMV_B1", "rows")
-        Bs = [1]
+    Bs = [1] if path.startswith("rows") else [1, 2, 4, 8, 16] if path == "f32" else [2, 4, 8, 16]
     w = S.quant_weights(qtype, M, K, seed=31, device=DEV)
     wn = w.cpu().numpy()
     for B in Bs:
         note(f"gemv {path} {QN[qtype]} B={B}")
         x = S.activations(B, K, seed=32 + B, device=DEV)
         y = torch.full((B, M), float("nan"), device=DEV)
-        qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t())
+        qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t(), x_f32=x_f32)
         torch.cuda.synchronize()
         ref = O.gemv_q_f64(qtype, wn, M, K, x.cpu().numpy())
-        assert_close(y.cpu().numpy().T, ref, tol=1e-4, what=f"{path} B={B}")
+        tol = 1e-5 if (x_f32 or path == "simt") else 1e-4
+        assert_close(y.cpu().numpy().T, ref, tol=tol, what=f"{path} B={B}")
+
+
+def test_gemv_flag_errors(qgemv):
+    M, K = 64, 4096
+    w = S.quant_weights(vx.VX_Q4_0, M, K, seed=1, device=DEV)
+    x = S.activations(1, K, seed=2, device=DEV)
+    y = torch.empty((M,), device=DEV)
+    with pytest.raises(vx.VortxError) as e:
+        qgemv.dispatch(y, vx.QWeight(w, vx.VX_Q4_0, M, K), x[0], x_f32=True, x_int8=True)
+    assert e.value.status == vx._ffi.VX_ERR_INVALID
+    yv, xv, wc = vx._view_of(y, True), vx._view_of(x[0], False), vx.QWeight(w, vx.VX_Q4_0, M, K)._c()
+    import ctypes as C
+    assert vx.lib().vx_gemv_q_ex(qgemv._h, None, C.byref(yv), C.byref(wc), C.byref(xv), 4) == vx._ffi.VX_ERR_INVALID
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])

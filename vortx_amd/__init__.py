@@ -236,12 +236,14 @@ class QWeight:
 class QuantGemv(_Context):
     """y = W x for GGML Q8_0 / Q4_0 / Q4_K weights, f32 accumulate."""
 
-    def dispatch(self, y, w: QWeight, x, stream=None, x_int8: bool = False) -> None:
-        """y = W x with f32 x and f32 accumulation. ``x_int8=True`` (batch 1)
-        selects the integer-dot path (x split into two int8 levels per
-        32-block, exact int32 block sums)."""
+    def dispatch(self, y, w: QWeight, x, stream=None, x_f32: bool = False, x_int8: bool = False) -> None:
+        """y = W x. By default x is split per 32-block into two int8 levels
+        (error <= 1.6e-5 of the block's max|x|) and every product is exact in
+        int32 (include/vortx_hip.h, vx_gemv_q_ex). ``x_f32=True`` keeps x in
+        f32 (f32 FMA on the exactly decoded weights); ``x_int8=True`` names
+        the default explicitly."""
         yv, xv, wc = _view_of(y, True), _view_of(x, False), w._c()
-        flags = _ffi.VX_GEMV_X_INT8 if x_int8 else 0
+        flags = (_ffi.VX_GEMV_X_F32 if x_f32 else 0) | (_ffi.VX_GEMV_X_INT8 if x_int8 else 0)
         check(lib().vx_gemv_q_ex(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags))
 
     def quantize(self, out: "QWeight", x, stream=None) -> None:

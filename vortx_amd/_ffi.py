@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(PKG, "libvortx_hip.so")
 VX_Q4_0, VX_Q8_0, VX_Q4_K = 2, 8, 12
 ROUTE_NAIVE, ROUTE_TILED, ROUTE_GEMV, ROUTE_EMPTY = range(4)
 NONE_STRIDE = 0xFFFFFFFF
-VX_GEMV_X_INT8 = 1
+VX_GEMV_X_INT8, VX_GEMV_X_F32 = 1, 2
 
 
 class VxLayout(C.Structure):

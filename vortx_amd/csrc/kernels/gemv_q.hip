@@ -268,13 +268,18 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
         const uint32_t us = act ? u : nunits - 1u;
         if (p != cur) {
             cur = p;
+            // The LDS addresses derive from a value defined inside this
+            // branch, so the compiler cannot hoist their arithmetic into every
+            // item (with one pass, K <= 4096, the branch runs once per wave).
+            uint32_t ul = us;
+            asm volatile("" : "+v"(ul));
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const f32x4 v = vx_lds_x[q * upitch + us];
+                const f32x4 v = vx_lds_x[q * upitch + ul];
                 xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
             }
-            sx0 = sxs[2u * us];
-            sx1 = sxs[2u * us + 1u];
+            sx0 = sxs[2u * ul];
+            sx1 = sxs[2u * ul + 1u];
         }
         const float d = vx_unit_dot_b1<QT>(w, xv, sx0, sx1, us);
         acc += act ? d : 0.f;
@@ -529,6 +534,151 @@ __device__ __forceinline__ void vx_gemv_i8b1(const vx_gemv_args& a) {
         for (int r = 0; r < R; ++r)
             if (rok[r]) a.y[(int64_t)(row0 + r) * a.ys_m] = acc[r];
     }
+}
+
+// Batch 1, persistent, on the integer-dot path: the work split, issue order
+// and ring of vx_gemv_p1, with x staged in LDS as two int8 levels per
+// 32-block (the vx_i8lds layout; x ~= c (254 x1 + x2), error <= c / 2 ~
+// 1.6e-5 of the block's max|x|). A unit then reduces in exact int32 with
+// v_dot4_i32_i8 (vx_unit_dot_i8): on gfx950 one v_dot4 (4 products) issues
+// in about the time of two v_fma_f32, and no weight is converted to float
+// (v_cvt_pk_f32_fp8 costs about three times a v_fma_f32), so a unit takes
+// about half the VALU time of vx_unit_dot_b1. Each 8 consecutive lanes
+// stage one 32-block; its max and sums are reduced with DPP.
+template <int QT, int P, int WGT, bool XV>
+__device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    constexpr int XPT = (int)(VX_P_XF / WGT);
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nwv = gridDim.x * (WGT / 64u);
+    const uint32_t gw = wave * gridDim.x + blockIdx.x;  // wave-major, as vx_gemv_p1
+    const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
+    const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
+    const uint32_t nitems = nrows * npass;
+    const vx_i8lds L{a.upitch, nunits};
+
+    // 1. x loads (float4 f = slot f & 15 of unit f >> 4), then the bare
+    //    barrier that puts them ahead of every weight request of the CU.
+    const uint32_t total = nunits * 16u;
+    f32x4 xr[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        if ((uint32_t)i * WGT >= total) break;  // uniform: rounds past x
+        const uint32_t f = min(t + WGT * (uint32_t)i, total - 1u);
+        if constexpr (XV) {
+            xr[i] = *(const f32x4*)(a.x + 4 * (int64_t)f);
+        } else {
+            const float* xp = a.x + 4 * (int64_t)f * a.xs_k;
+            xr[i] = f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
+        }
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    // 2. the first ring items (see vx_gemv_p1 for the clamping).
+    const uint8_t* wbase = a.w;
+    auto item_ptr = [&](uint32_t it, uint32_t& unit) {
+        const uint32_t c = nitems ? min(it, nitems - 1u) : 0u;
+        const uint32_t ri = c / npass, p = c - ri * npass;
+        const uint32_t row = min(gw + ri * nwv, a.M - 1u);
+        unit = it < nitems ? min(64u * p + lane, nunits - 1u) : 0u;
+        return wbase + (uint64_t)row * a.row_stride;
+    };
+    constexpr int PRE = P <= 2 ? P : 1;
+    uint32_t wr[P][NW];
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+        uint32_t u;
+        const uint8_t* rp = item_ptr((uint32_t)j, u);
+        vx_load_unit<QT>(rp, u, wr[j]);
+    }
+
+    // 3. split x into the two levels and store them with the block scale c,
+    //    sum(x) and O = sum(254 x1 + x2) (|O| < 2^21: exact as a float sum).
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        if ((uint32_t)i * WGT >= total) break;
+        const uint32_t f = t + WGT * (uint32_t)i;
+        const bool in = f < total;
+        const f32x4 v = in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+        const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float c = m * (1.0f / (127.0f * 254.0f));
+        const float inv1 = m > 0.f ? 127.0f / m : 0.f;  // 1 / (254 c)
+        const float inv2 = inv1 * 254.0f;               // 1 / c
+        const float s1 = 254.0f * c;
+        int q1[4], q2[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            q1[e] = (int)rintf(v[e] * inv1);
+            const float r = __builtin_fmaf(-(float)q1[e], s1, v[e]);
+            q2[e] = min(127, max(-127, (int)rintf(r * inv2)));
+        }
+        const float sx = vx_sum8((v.x + v.y) + (v.z + v.w));
+        const float oz = vx_sum8((float)(254 * (q1[0] + q1[1] + q1[2] + q1[3]) + (q2[0] + q2[1] + q2[2] + q2[3])));
+        if (in) {
+            const uint32_t ul = f >> 4, j = f & 15u;
+            uint32_t* x8 = (uint32_t*)L.x8(0);
+            x8[((0u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[0], q1[1], q1[2], q1[3]);
+            x8[((1u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
+            if ((j & 7u) == 0u) {
+                const uint32_t idx = 2u * ul + (j >> 3);
+                L.cs(1, 0)[idx] = c;
+                L.sx(1, 0)[idx] = sx;
+                L.oz(1, 0)[idx] = (int)oz;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. the rest of the ring, then stream the items (whole rounds of P in
+    //    the main loop: exact wait counts; the last partial round follows).
+#pragma unroll
+    for (int j = PRE; j < P; ++j) {
+        uint32_t u;
+        const uint8_t* rp = item_ptr((uint32_t)j, u);
+        vx_load_unit<QT>(rp, u, wr[j]);
+    }
+    uint32_t x1[16], x2[16];
+    float cb[2], sxb[2];
+    int ozb[2];
+    uint32_t cur = ~0u;
+    float acc = 0.f;
+    auto body = [&](uint32_t it, uint32_t (&w)[NW]) {
+        const uint32_t ri = it / npass, p = it - ri * npass;
+        const uint32_t u = 64u * p + lane;
+        const bool act = u < nunits;
+        const uint32_t us = act ? u : nunits - 1u;
+        if (p != cur) {
+            cur = p;
+            uint32_t ul = us;  // defined in the branch: its LDS addressing stays here
+            asm volatile("" : "+v"(ul));
+            vx_read_x8(L, 0, ul, x1, x2);
+            const float2 cb2 = *(const float2*)&L.cs(1, 0)[2u * ul];
+            const float2 sx2 = *(const float2*)&L.sx(1, 0)[2u * ul];
+            const int2 oz2 = *(const int2*)&L.oz(1, 0)[2u * ul];
+            cb[0] = cb2.x; cb[1] = cb2.y; sxb[0] = sx2.x; sxb[1] = sx2.y; ozb[0] = oz2.x; ozb[1] = oz2.y;
+        }
+        const float d = vx_unit_dot_i8<QT>(w, x1, x2, cb, sxb, ozb, us);
+        acc += act ? d : 0.f;
+        uint32_t nu;
+        const uint8_t* rp = item_ptr(it + P, nu);
+        vx_load_unit<QT>(rp, nu, w);
+        if (p == npass - 1u) {
+            const float sum = vx_wave_sum(acc);
+            if (lane == 0) a.y[(int64_t)(gw + ri * nwv) * a.ys_m] = sum;
+            acc = 0.f;
+        }
+    };
+    const uint32_t nfull = nitems - nitems % P;
+    for (uint32_t it0 = 0; it0 < nfull; it0 += P) {
+#pragma unroll
+        for (int j = 0; j < P; ++j) body(it0 + (uint32_t)j, wr[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < P - 1; ++j)
+        if (nfull + (uint32_t)j < nitems) body(nfull + (uint32_t)j, wr[j]);
 }
 
 // Batch NB > 1: lane l serves row group g = l / LPR (R rows each) and unit
@@ -979,6 +1129,10 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(vx_gemv_args a) {  \
         if (a.x_vec) vx_gemv_p1<QT, P, WGT, true>(a); else vx_gemv_p1<QT, P, WGT, false>(a);   \
     }
+#define VX_GEMV_P1I(QT, QN, P)                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(vx_gemv_args a) {  \
+        if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true>(a); else vx_gemv_p1i<QT, P, 1024, false>(a); \
+    }
 #define VX_GEMV_I8B(QT, QN, NCP)                                                                \
     extern "C" __global__ __launch_bounds__(VX_B_WG) void vx_gemv_i8b_##QN##_c##NCP(vx_gemv_args a) { \
         if (a.x_vec) vx_gemv_i8b<QT, NCP, true>(a); else vx_gemv_i8b<QT, NCP, false>(a);        \
@@ -1010,6 +1164,12 @@ VX_GEMV_P1(VX_Q4_K, q4_k, 2, 1024)
 VX_GEMV_P1(VX_Q4_0, q4_0, 4, 512)
 VX_GEMV_P1(VX_Q8_0, q8_0, 3, 512)
 VX_GEMV_P1(VX_Q4_K, q4_k, 4, 512)
+VX_GEMV_P1I(VX_Q4_0, q4_0, 2)
+VX_GEMV_P1I(VX_Q4_0, q4_0, 3)
+VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
+VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
+VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
+VX_GEMV_P1I(VX_Q4_K, q4_k, 3)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 1)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 2)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 4)

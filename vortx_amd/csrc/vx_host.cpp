@@ -421,6 +421,15 @@ static int p1_kernel(uint32_t qt, int wgt) {
     return tab[q_index(qt)][wgt == 1024 ? 0 : 1];
 }
 
+// Persistent batch-1 kernel on the integer-dot path, by ring depth P.
+static int p1i_kernel(uint32_t qt, int P) {
+    switch (q_index(qt)) {
+    case 0: return P >= 3 ? K_vx_gemv_p1i_q4_0_p3 : K_vx_gemv_p1i_q4_0_p2;
+    case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
+    default: return P >= 3 ? K_vx_gemv_p1i_q4_k_p3 : K_vx_gemv_p1i_q4_k_p2;
+    }
+}
+
 static int i8b_kernel(uint32_t qt, uint32_t B) {
     static const int tab[3][3] = {
         {K_vx_gemv_i8b_q4_0_c1, K_vx_gemv_i8b_q4_0_c2, K_vx_gemv_i8b_q4_0_c4},
@@ -499,8 +508,11 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
 
     const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
+    // x as two int8 levels per 32-block (the default) or exact f32
+    // (VX_GEMV_X_F32, or VX_GEMV_BATCHED=simt for batches only)
+    const bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
     const char* bmode = std::getenv("VX_GEMV_BATCHED");
-    const bool force_simt = bmode && std::strcmp(bmode, "simt") == 0;
+    const bool force_simt = x_f32 || (bmode && std::strcmp(bmode, "simt") == 0);
     if (B >= 2 && fast && !force_simt) {
         // int8 matrix-core path, one workgroup per CU, up to 8 columns per
         // launch (fewer when x of that many columns does not fit LDS).
@@ -524,7 +536,8 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         }
     }
     // batch-1 kernel: the persistent one (default), or the per-row-group
-    // one with VX_GEMV_B1=rows (also used when x does not fit its LDS)
+    // one with VX_GEMV_B1=rows (also used when x does not fit its LDS:
+    // K > 16384); int8 x unless VX_GEMV_X_F32
     const char* b1env = std::getenv("VX_GEMV_B1");
     const bool b1_rows = b1env && std::strcmp(b1env, "rows") == 0;
     uint32_t b0 = 0;
@@ -542,7 +555,16 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         int k;
         uint32_t rows_per_wg;
         size_t lds;
-        if (NB == 1 && (flags & VX_GEMV_X_INT8)) {
+        if (NB == 1 && !x_f32 && a.nunits <= 256u && !b1_rows) {
+            // persistent integer-dot path: all of x as int8 levels, 152 B per unit
+            a.chunk_units = a.nunits;
+            a.upitch = a.nunits | 1u;
+            lds = (size_t)a.upitch * 152u;
+            s = launch(ctx, p1i_kernel(w->qtype, 2), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
+            if (s) return s;
+            b0 += NB;
+            continue;
+        } else if (NB == 1 && !x_f32) {
             // integer-dot path: 152 bytes of LDS per staged unit
             const int R = pick_rows_per_wave(ctx, w->qtype, M);
             uint32_t cu = a.nunits;
@@ -796,7 +818,9 @@ int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight*
 
 int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
                  uint32_t flags) {
-    if (flags & ~(uint32_t)VX_GEMV_X_INT8) return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_ex flags");
+    if (flags & ~(uint32_t)(VX_GEMV_X_INT8 | VX_GEMV_X_F32)) return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_ex flags");
+    if ((flags & VX_GEMV_X_INT8) && (flags & VX_GEMV_X_F32))
+        return vx::fail(VX_ERR_INVALID, "VX_GEMV_X_INT8 and VX_GEMV_X_F32 are exclusive");
     return vx::run_gemv_q(ctx, stream, y, w, x, flags);
 }
 
