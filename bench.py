@@ -7,12 +7,14 @@ next of >= 512 MB of distinct weight copies (so the 256 MB Infinity Cache
 cannot serve them), inputs resident in HBM before timing starts.
 
 Secondary lines in the same JSON object: the other BASELINE GEMV configs
-(Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 b=1, Q4_0 11008 x 4096
-b=8, Q4_K 14336 x 4096 b=16; GB/s of algorithmic bytes), the contiguous
-copy of a transposed 8192^2 view, the Q8_0 and Q4_K quantizers on
-14336 x 4096, the GGUF file -> HBM upload (against the PCIe 5.0 x16 link)
-and the f32 GEMM 4096^3 (TFLOP/s), each with its roofline, plus CPU
-baselines from the oracle's OpenMP restatements on the host cores.
+(Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 and 14336 x 4096 b=1,
+Q4_0 4096 x 11008 b=1, Q4_0 11008 x 4096 b=4 and b=8, Q4_K 14336 x 4096
+b=16; GB/s of algorithmic bytes), the contiguous copy of a transposed
+8192^2 view, the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
+-> HBM upload (against the PCIe 5.0 x16 link) and the f32 GEMMs 4096^3,
+4096 x 11008 x 4096, 4096^3 with a transposed-B view and the broadcast
+batch (TFLOP/s), each with its roofline, plus CPU baselines from the
+oracle's OpenMP restatements on the host cores.
 
 Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
 (captured eager launches) between two synchronizations (wall clock).
@@ -121,7 +123,9 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     }
 
 
-def time_gemm(M: int, N: int, K: int, steps: int, warmup: int):
+def time_gemm(M: int, N: int, K: int, steps: int, warmup: int, transb: bool = False):
+    """C = A B with row-major A [M, K]; B is row-major [K, N], or with transb the
+    stride-swapped view of an [N, K] buffer (the reference's transposed-B case)."""
     import torch
 
     import vortx_amd as vx
@@ -129,7 +133,7 @@ def time_gemm(M: int, N: int, K: int, steps: int, warmup: int):
 
     dev = torch.device("cuda:0")
     a = S.uniform((M, K), 1, dev)
-    b = S.uniform((K, N), 2, dev)
+    b = S.uniform((N, K), 2, dev).t() if transb else S.uniform((K, N), 2, dev)
     c = torch.empty((M, N), device=dev)
     gm = vx.Gemm(0)
     for _ in range(warmup):
@@ -338,6 +342,9 @@ def main() -> int:
     SECONDARY = [
         (8, 4096, 4096, 1, "q8_0", "Q8_0 GEMV 4096x4096 batch 1", "gemv_q8_0_4096x4096_b1"),
         (12, 32000, 4096, 1, "q4_k", "Q4_K GEMV 32000x4096 batch 1", "gemv_q4_k_32000x4096_b1"),
+        (2, 4096, 11008, 1, "q4_0_t", "Q4_0 GEMV 4096x11008 batch 1", "gemv_q4_0_4096x11008_b1"),
+        (12, 14336, 4096, 1, "q4_k_14336", "Q4_K GEMV 14336x4096 batch 1", "gemv_q4_k_14336x4096_b1"),
+        (2, 11008, 4096, 4, "q4_0_b4", "Q4_0 GEMV 11008x4096 batch 4", "gemv_q4_0_11008x4096_b4"),
         (2, 11008, 4096, 8, "q4_0_b8", "Q4_0 GEMV 11008x4096 batch 8", "gemv_q4_0_11008x4096_b8"),
         (8, 4096, 4096, 8, "q8_0_b8", "Q8_0 GEMV 4096x4096 batch 8", "gemv_q8_0_4096x4096_b8"),
         (12, 14336, 4096, 16, "q4_k_b16", "Q4_K GEMV 14336x4096 batch 16", "gemv_q4_k_14336x4096_b16"),
@@ -351,6 +358,10 @@ def main() -> int:
     gsteps = max(5, min(50, args.steps // 40))
     gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm] {gemm}")
+    gemm_n = time_gemm(4096, 11008, 4096, gsteps, max(2, args.warmup // 100))
+    log(f"[gemm_4096x11008x4096] {gemm_n}")
+    gemm_t = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100), transb=True)
+    log(f"[gemm_transb] {gemm_t}")
     gemm_b = time_gemm_broadcast(8, 1024, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm_broadcast] {gemm_b}")
     cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
@@ -374,8 +385,11 @@ def main() -> int:
         return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(name)}
 
-    gemm_ach = gemm["flops"] / (gemm["avg_launch_ms"] * 1e-3) / 1e12
-    gemm_b_ach = gemm_b["flops"] / (gemm_b["avg_launch_ms"] * 1e-3) / 1e12
+    def roof_mfma(r, name):
+        achieved = r["flops"] / (r["avg_launch_ms"] * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": achieved, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                "frac": achieved / F32_MFMA_PEAK_TFS, "traffic": load_traffic(name)}
+
     line = {
         "metric": METRIC,
         "value": q40["value"],
@@ -416,14 +430,18 @@ def main() -> int:
         ] + [
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
-             "roofline": {"bound": "mfma", "achieved": gemm_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
-                          "frac": gemm_ach / F32_MFMA_PEAK_TFS, "traffic": load_traffic("gemm_f32_4096")},
+             "roofline": roof_mfma(gemm, "gemm_f32_4096"),
              "cpu_baseline": cpu["gemm1024"] if cpu else None},
+            {"workload": "f32 GEMM M=4096 N=11008 K=4096 (row-major A, B)", "value": gemm_n["value"],
+             "unit": "TFLOP/s", "ms_per_step": gemm_n["ms_per_step"],
+             "roofline": roof_mfma(gemm_n, "gemm_f32_4096x11008x4096")},
+            {"workload": "f32 GEMM 4096^3, B a transposed view of a row-major [N, K] buffer", "value": gemm_t["value"],
+             "unit": "TFLOP/s", "ms_per_step": gemm_t["ms_per_step"],
+             "roofline": roof_mfma(gemm_t, "gemm_f32_4096_transb")},
             {"workload": "broadcast f32 GEMM out[b] = A[b] W + out[b], A [8, 1024, 4096], shared W [4096, 4096] "
                          "(vx_gemm_f32_ex, beta = 1)", "value": gemm_b["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm_b["ms_per_step"],
-             "roofline": {"bound": "mfma", "achieved": gemm_b_ach, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
-                          "frac": gemm_b_ach / F32_MFMA_PEAK_TFS, "traffic": load_traffic("gemm_f32_broadcast_8x1024")}},
+             "roofline": roof_mfma(gemm_b, "gemm_f32_broadcast_8x1024")},
         ],
     }
     print(json.dumps(line), flush=True)
