@@ -796,7 +796,18 @@ __device__ __forceinline__ void vx_gemv_bn(const vx_gemv_args& a) {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 #define VX_B_WG 1024
-#define VX_B_XPT 8  // float4 of x per thread loaded ahead of the weight stream
+
+// 1.5 * 2^23: fmaf(v, s, VX_RND_MAGIC) rounds v s to the nearest integer n
+// (ties to even) for |v s| < 2^22, leaving n - VX_RND_MAGIC exact and the
+// low byte of the float's bits equal to n & 0xFF (the int8 of n).
+#define VX_RND_MAGIC 12582912.0f
+
+// Low bytes of four floats from fmaf(., ., VX_RND_MAGIC), packed.
+__device__ __forceinline__ uint32_t vx_pack_lo_bytes(const float (&t)[4]) {
+    const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(t[1]), __float_as_uint(t[0]), 0x0C0C0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(t[3]), __float_as_uint(t[2]), 0x04000C0Cu);
+    return lo | hi;
+}
 
 // B operand for piece s (elements 16s..16s+15) of a unit held in r.
 template <int QT, int S>
@@ -882,22 +893,26 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     float* red = (float*)(scl + B * nunits);
     if (t < 16u) ((uint32_t*)(xq + a.upitch))[t] = 0u;
 
-    // 1. x: float4 f = (column f / (16 nunits), unit, slot); the first
-    //    VX_B_XPT per thread are loaded before the issue-order barrier.
-    const uint32_t per_col = nunits * 16u, total = B * per_col;
-    auto xload = [&](uint32_t f) {
-        const uint32_t col = f / per_col, rem = f - col * per_col;
-        const int64_t k = 4 * (int64_t)rem;  // 64 u + 4 slot
-        if constexpr (XV) return *(const f32x4*)(a.x + (int64_t)col * a.xs_b + k);
-        const float* xp = a.x + (int64_t)col * a.xs_b + k * a.xs_k;
-        return f32x4{xp[0], xp[a.xs_k], xp[2 * a.xs_k], xp[3 * a.xs_k]};
-    };
-    f32x4 xr[VX_B_XPT];
+    // 1. x: block g = 32-block g % bpc of column g / bpc. Thread t splits
+    //    blocks t, t + 1024, ...; the first one is loaded before the
+    //    issue-order barrier.
+    const uint32_t bpc = 2u * nunits, nblk = B * bpc;
+    auto xload = [&](uint32_t g, f32x4 (&v)[8]) {
+        const uint32_t col = g / bpc, blk = g - col * bpc;
+        if constexpr (XV) {
+            const f32x4* xp = (const f32x4*)(a.x + (int64_t)col * a.xs_b + 32 * (int64_t)blk);
 #pragma unroll
-    for (int i = 0; i < VX_B_XPT; ++i) {
-        if ((uint32_t)i * VX_B_WG >= total) break;  // uniform
-        xr[i] = xload(min(t + VX_B_WG * (uint32_t)i, total - 1u));
-    }
+            for (int i = 0; i < 8; ++i) v[i] = xp[i];
+        } else {
+            const float* xp = a.x + (int64_t)col * a.xs_b + 32 * (int64_t)blk * a.xs_k;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                v[i] = f32x4{xp[(4 * i) * a.xs_k], xp[(4 * i + 1) * a.xs_k], xp[(4 * i + 2) * a.xs_k],
+                             xp[(4 * i + 3) * a.xs_k]};
+        }
+    };
+    f32x4 xr[8];
+    xload(min(t, nblk - 1u), xr);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -926,44 +941,48 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     vx_load_unit<QT>(prow, unit_of(0u), wr[0]);
     padv();
 
-    // 2. split x into two int8 levels per 32-block (8 float4 = 8 lanes).
-    auto split = [&](uint32_t f, f32x4 v, bool in) {
-        if (!in) v = f32x4{0.f, 0.f, 0.f, 0.f};
-        const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        const float ps = vx_sum8((v.x + v.y) + (v.z + v.w));
+    // 2. split each block into two int8 levels: x ~= c2 (254 q1 + q2) with
+    //    c1 = max|x| / 126, c2 = c1 / 254, q1 = rnd(x / c1), q2 = rnd((x -
+    //    q1 c1) / c2); |x / c1 - q1| <= 1/2 (plus rounding of the reciprocal)
+    //    keeps |q2| <= 127. Blocks with max|x| < 2^-100 are stored as zero.
+    auto split = [&](uint32_t g, const f32x4 (&v)[8]) {
+        float m = 0.f, s4[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+            s4[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        }
+        const float ps = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]));
         const bool fin = m < __builtin_inff();
         const float c1 = m * (1.f / 126.f), c2 = c1 * (1.f / 254.f);
-        const float i1 = (fin && m > 0.f) ? 126.f / m : 0.f, i2 = i1 * 254.f;
-        uint32_t pk0 = 0, pk1 = 0;
+        const float i1 = (fin && m >= 0x1p-100f) ? 126.f * __builtin_amdgcn_rcpf(m) : 0.f, i2 = i1 * 254.f;
+        uint32_t l0[8], l1[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float q1 = __builtin_rintf(v[e] * i1);
-            const float r1 = __builtin_fmaf(-q1, c1, v[e]);
-            const float q2 = __builtin_rintf(r1 * i2);
-            pk0 |= ((uint32_t)(int)q1 & 0xFFu) << (8 * e);
-            pk1 |= ((uint32_t)(int)q2 & 0xFFu) << (8 * e);
-        }
-        if (in) {
-            const uint32_t cu_ = f >> 4, w4 = f & 15u;  // cu_ = column * nunits + unit
-            uint32_t* xu = (uint32_t*)(xq + 128u * cu_) + w4;
-            xu[0] = pk0;
-            xu[16] = pk1;
-            if ((f & 7u) == 0u) {
-                float* sc = (float*)(scl + cu_) + 2u * (w4 >> 3);
-                sc[0] = fin ? c2 : m;  // non-finite x: propagate into y
-                sc[1] = ps;
+        for (int i = 0; i < 8; ++i) {
+            float t1[4], t2[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                t1[e] = __builtin_fmaf(v[i][e], i1, VX_RND_MAGIC);
+                const float r1 = __builtin_fmaf(-(t1[e] - VX_RND_MAGIC), c1, v[i][e]);
+                t2[e] = __builtin_fmaf(r1, i2, VX_RND_MAGIC);
             }
+            l0[i] = vx_pack_lo_bytes(t1);
+            l1[i] = vx_pack_lo_bytes(t2);
         }
+        const uint32_t col = g / bpc, blk = g - col * bpc;
+        const uint32_t cu_ = col * nunits + (blk >> 1), h = blk & 1u;
+        uint4* xu = (uint4*)(xq + 128u * cu_ + 32u * h);
+        xu[0] = uint4{l0[0], l0[1], l0[2], l0[3]};
+        xu[1] = uint4{l0[4], l0[5], l0[6], l0[7]};
+        xu[4] = uint4{l1[0], l1[1], l1[2], l1[3]};
+        xu[5] = uint4{l1[4], l1[5], l1[6], l1[7]};
+        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m, ps};  // non-finite x: into y
     };
-#pragma unroll
-    for (int i = 0; i < VX_B_XPT; ++i) {
-        if ((uint32_t)i * VX_B_WG >= total) break;
-        const uint32_t f = t + VX_B_WG * (uint32_t)i;
-        split(f, xr[i], f < total);
-    }
-    for (uint32_t f0 = VX_B_XPT * VX_B_WG; f0 < total; f0 += VX_B_WG) {
-        const uint32_t f = f0 + t;
-        split(f, xload(min(f, total - 1u)), f < total);
+    if (t < nblk) split(t, xr);
+    for (uint32_t g = t + VX_B_WG; g < nblk; g += VX_B_WG) {
+        f32x4 v[8];
+        xload(g, v);
+        split(g, v);
     }
     __syncthreads();
 
@@ -1003,17 +1022,15 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
                 const i32x4 bw1 = bb ? vx_m_piece<QT, 3>(r) : vx_m_piece<QT, 1>(r);
 #pragma unroll
                 for (int cp = 0; cp < NCP; ++cp) {
-                    // only the 16 lanes of k-group rows read LDS; the rest are zero
-                    i32x4 a0 = z, a1 = z;
-                    if (a_on && abase[cp] != a.upitch) {
-                        const uint8_t* ap = xq + abase[cp] + 32u * bb;
-                        a0 = *(const i32x4*)ap;
-                        a1 = *(const i32x4*)(ap + 16u);
-                    }
+                    // lanes outside their k-group's A rows (and columns >= B)
+                    // read the 64 zero bytes at a.upitch
+                    const uint8_t* ap = xq + abase[cp] + 32u * bb;
+                    const i32x4 a0 = *(const i32x4*)ap;
+                    const i32x4 a1 = *(const i32x4*)(ap + 16u);
                     i32x4 dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bw0, z, 0, 0, 0);
                     dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bw1, dd, 0, 0, 0);
-                    tq[cp][0][bb] = (float)(254 * dd[0] + dd[1]);
-                    tq[cp][1][bb] = (float)(254 * dd[2] + dd[3]);
+                    tq[cp][0][bb] = (float)(__mul24(dd[0], 254) + dd[1]);
+                    tq[cp][1][bb] = (float)(__mul24(dd[2], 254) + dd[3]);
                 }
             }
             float st[2], so[2];
@@ -1041,13 +1058,16 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
         vx_load_unit<QT>(prow, unit_of(pk), rl);
         padv();
         if (++k == upw) {
-            // row j's sums over the four units of this wave's rounds
+            // row j's sums over the four units of this wave's rounds, four
+            // columns at a time: row r of the result is column c0 + r
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float v = vx_sum_rows4(acc[c]);
-                if ((uint32_t)c < B && lane < 16u) red[((ts * 16u + wave) * B + c) * 16u + lane] = v;
-                acc[c] = 0.f;
+            for (int c0 = 0; c0 < NC; c0 += 4) {
+                const float v = vx_sum_rows4x4(acc[c0], acc[c0 + 1], c0 + 2 < NC ? acc[c0 + 2] : 0.f,
+                                               c0 + 3 < NC ? acc[c0 + 3] : 0.f);
+                if ((uint32_t)c0 + (lane >> 4) < B) red[((ts * 16u + wave) * B + (uint32_t)c0) * 16u + lane] = v;
             }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[c] = 0.f;
             k = 0;
             ++ts;
         }

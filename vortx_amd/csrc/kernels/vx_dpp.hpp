@@ -70,3 +70,26 @@ __device__ __forceinline__ float vx_sum_rows4(float v) {
     vx_pin2(b0, b1);
     return __builtin_bit_cast(float, b0) + __builtin_bit_cast(float, b1);
 }
+
+// vx_sum_rows4 of four values at once: row r (lanes 16r..16r+15) of the
+// result holds the row sums of v_r, lane l having v_r[l % 16] + v_r[l % 16
+// + 16] + v_r[l % 16 + 32] + v_r[l % 16 + 48], added in the same order as
+// vx_sum_rows4. The first permlane16_swap pairs v0 with v1 and v2 with v3
+// (row sums of rows 0 + 1 and 2 + 3 of each), the permlane32_swap pairs the
+// two results: three swaps and three adds for four values.
+__device__ __forceinline__ float vx_sum_rows4x4(float v0, float v1, float v2, float v3) {
+    auto pair16 = [](float x, float y) {
+        unsigned a = __builtin_bit_cast(unsigned, x), b = __builtin_bit_cast(unsigned, y);
+        vx_pin2(a, b);
+        const auto s = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        unsigned s0 = s[0], s1 = s[1];
+        vx_pin2(s0, s1);
+        return __builtin_bit_cast(float, s0) + __builtin_bit_cast(float, s1);
+    };
+    unsigned p = __builtin_bit_cast(unsigned, pair16(v0, v1)), q = __builtin_bit_cast(unsigned, pair16(v2, v3));
+    vx_pin2(p, q);
+    const auto t = __builtin_amdgcn_permlane32_swap(p, q, false, false);
+    unsigned t0 = t[0], t1 = t[1];
+    vx_pin2(t0, t1);
+    return __builtin_bit_cast(float, t0) + __builtin_bit_cast(float, t1);
+}
