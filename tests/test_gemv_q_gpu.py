@@ -261,3 +261,26 @@ def test_gemv_shape_errors(qgemv):
     bad.qtype = 3  # not a supported GGML type
     with pytest.raises(vx.VortxError, match="VX_ERR_INVALID"):
         qgemv.dispatch(torch.zeros(M, device=DEV), bad, torch.zeros(K, device=DEV))
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), -float("inf")], ids=["nan", "inf", "-inf"])
+def test_non_finite_x_reaches_its_column_only(qgemv, qtype, B, bad):
+    """One non-finite value in column 0 of x makes every y of that column
+    non-finite, on the int8 path at batch 1 and on the batched kernel; the
+    other columns equal a run without it, bit for bit."""
+    M, K = 300, 2048
+    note(f"gemv non-finite x {QN[qtype]} B={B} {bad}")
+    w = vx.QWeight(S.quant_weights(qtype, M, K, seed=5, device=DEV), qtype, M, K)
+    x = S.activations(B, K, seed=6, device=DEV)
+    y0 = torch.empty((B, M), device=DEV)
+    qgemv.dispatch(y0.t(), w, x.t())
+    xb = x.clone()
+    xb[0, 777] = bad
+    y = torch.empty((B, M), device=DEV)
+    qgemv.dispatch(y.t(), w, xb.t())
+    torch.cuda.synchronize()
+    assert not torch.isfinite(y[0]).any(), "a non-finite x value was lost"
+    if B > 1:
+        assert torch.equal(y[1:].view(torch.int32), y0[1:].view(torch.int32))

@@ -616,6 +616,9 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
             q2[e] = min(127, max(-127, (int)rintf(r * inv2)));
         }
         const float sx = vx_sum8((v.x + v.y) + (v.z + v.w));
+        // a non-finite block (fmaxf skips NaN; the sum does not) stores
+        // max + sum as its scale, so y is non-finite
+        const bool fin = m < __builtin_inff() && sx == sx;
         const float oz = vx_sum8((float)(254 * (q1[0] + q1[1] + q1[2] + q1[3]) + (q2[0] + q2[1] + q2[2] + q2[3])));
         if (in) {
             const uint32_t ul = f >> 4, j = f & 15u;
@@ -624,7 +627,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
             x8[((1u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
             if ((j & 7u) == 0u) {
                 const uint32_t idx = 2u * ul + (j >> 3);
-                L.cs(1, 0)[idx] = c;
+                L.cs(1, 0)[idx] = fin ? c : m + sx;
                 L.sx(1, 0)[idx] = sx;
                 L.oz(1, 0)[idx] = (int)oz;
             }
@@ -953,7 +956,7 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
             s4[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
         }
         const float ps = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]));
-        const bool fin = m < __builtin_inff();
+        const bool fin = m < __builtin_inff() && ps == ps;  // fmaxf skips NaN; the sum does not
         const float c1 = m * (1.f / 126.f), c2 = c1 * (1.f / 254.f);
         const float i1 = (fin && m >= 0x1p-100f) ? 126.f * __builtin_amdgcn_rcpf(m) : 0.f, i2 = i1 * 254.f;
         uint32_t l0[8], l1[8];
@@ -976,7 +979,7 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
         xu[1] = uint4{l0[4], l0[5], l0[6], l0[7]};
         xu[4] = uint4{l1[0], l1[1], l1[2], l1[3]};
         xu[5] = uint4{l1[4], l1[5], l1[6], l1[7]};
-        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m, ps};  // non-finite x: into y
+        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m + ps, ps};  // non-finite x: into y
     };
     if (t < nblk) split(t, xr);
     for (uint32_t g = t + VX_B_WG; g < nblk; g += VX_B_WG) {
