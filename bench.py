@@ -10,7 +10,8 @@ Secondary lines in the same JSON object: the other BASELINE GEMV configs
 (Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 and 14336 x 4096 b=1,
 Q4_0 4096 x 11008 b=1, Q4_0 11008 x 4096 b=4 and b=8, Q4_K 14336 x 4096
 b=16; GB/s of algorithmic bytes), the contiguous copy of a transposed
-8192^2 view, the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
+8192^2 view and a plain streaming copy of a contiguous one (the achievable
+bandwidth beside the 8 TB/s peak), the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
 -> HBM upload (against the PCIe 5.0 x16 link) and the f32 GEMMs 4096^3,
 4096 x 11008 x 4096, 4096^3 with a transposed-B view and the broadcast
 batch (TFLOP/s), each with its roofline, plus CPU baselines from the
@@ -185,15 +186,19 @@ def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int)
             "ms_per_step": wall * 1e3 / steps}
 
 
-def time_contiguous(shape, steps: int, warmup: int):
+def time_contiguous(shape, steps: int, warmup: int, transposed: bool = True):
     """vortx's Contiguous op (src/linalg/contiguous.rs) on a transposed f32
-    view: bytes = 8 per element (read + write); 4 rotating 256 MB sources."""
+    view, or (transposed=False) on a contiguous one, where it is a plain
+    streaming copy (the achievable-bandwidth reference): bytes = 8 per
+    element (read + write); 4 rotating 256 MB sources."""
     import torch
 
     import vortx_amd as vx
 
     dev = torch.device("cuda:0")
-    srcs = [torch.randn(shape, device=dev).t() for _ in range(4)]
+    srcs = [torch.randn(shape, device=dev) for _ in range(4)]
+    if transposed:
+        srcs = [t.t() for t in srcs]
     out = torch.empty(srcs[0].shape, device=dev)
     c = vx.Contiguous(0)
     for i in range(warmup):
@@ -316,6 +321,17 @@ def cpu_baselines(threads: int):
     out["gemm1024"] = {"value": 2.0 * 1024 ** 3 / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
                        "sample": "10 timed (3 warmup) f32 GEMM 1024^3, OpenMP restatement of gemm_tiled "
                                  "(64x64x16 tiles, reference k order)"}
+    for M, N, K, key in ((4096, 4096, 4096, "gemm4096"), (4096, 11008, 4096, "gemm4096x11008")):
+        a = np.random.default_rng(1).uniform(-1, 1, (M, K)).astype(np.float32)
+        b = np.random.default_rng(2).uniform(-1, 1, (K, N)).astype(np.float32)
+        O.gemm_tiled_f32_omp(a, b, threads)  # 1 warmup + 3 timed for the 4096-class shapes
+        t0 = time.perf_counter()
+        for _ in range(3):
+            O.gemm_tiled_f32_omp(a, b, threads)
+        dt = (time.perf_counter() - t0) / 3
+        out[key] = {"value": 2.0 * M * N * K / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                    "sample": f"3 timed (1 warmup) f32 GEMM {M}x{N}x{K}, OpenMP restatement of gemm_tiled "
+                              f"(64x64x16 tiles, reference k order)"}
     return out
 
 
@@ -366,6 +382,8 @@ def main() -> int:
     log(f"[gemm_broadcast] {gemm_b}")
     cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
     log(f"[contiguous] {cont}")
+    copy = time_contiguous((8192, 8192), max(10, args.steps // 20), 5, transposed=False)
+    log(f"[copy] {copy}")
     quant = []
     for qt, label in ((8, "q8_0"), (12, "q4_k")):
         r = time_quantize(qt, 14336, 4096, max(10, args.steps // (20 if qt == 8 else 100)), 3)
@@ -415,6 +433,10 @@ def main() -> int:
             {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
              "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],
              "roofline": roof_hbm(cont, "contiguous_t8192")},
+            {"workload": "streaming copy: Contiguous::launch of a contiguous 8192x8192 f32 view (achievable HBM "
+                         "bandwidth of a plain read + write stream on this GPU)",
+             "value": copy["value"], "unit": "GB/s", "ms_per_step": copy["ms_per_step"],
+             "roofline": roof_hbm(copy, "copy_8192")},
         ] + [
             {"workload": f"quantize f32 14336x4096 to {label.upper()} blocks (ggml reference quantizer)",
              "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
@@ -431,10 +453,12 @@ def main() -> int:
             {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm["ms_per_step"],
              "roofline": roof_mfma(gemm, "gemm_f32_4096"),
-             "cpu_baseline": cpu["gemm1024"] if cpu else None},
+             "cpu_baseline": cpu["gemm4096"] if cpu else None,
+             "cpu_baseline_1024": cpu["gemm1024"] if cpu else None},
             {"workload": "f32 GEMM M=4096 N=11008 K=4096 (row-major A, B)", "value": gemm_n["value"],
              "unit": "TFLOP/s", "ms_per_step": gemm_n["ms_per_step"],
-             "roofline": roof_mfma(gemm_n, "gemm_f32_4096x11008x4096")},
+             "roofline": roof_mfma(gemm_n, "gemm_f32_4096x11008x4096"),
+             "cpu_baseline": cpu["gemm4096x11008"] if cpu else None},
             {"workload": "f32 GEMM 4096^3, B a transposed view of a row-major [N, K] buffer", "value": gemm_t["value"],
              "unit": "TFLOP/s", "ms_per_step": gemm_t["ms_per_step"],
              "roofline": roof_mfma(gemm_t, "gemm_f32_4096_transb")},
