@@ -42,6 +42,9 @@ def test_reference_contiguous_transpose(cont):
     ((2, 3, 40, 33), (3, 2, 1, 0)),
     ((5, 1000), (1, 0)),
     ((1000, 5), (1, 0)),
+    ((3, 200, 132), (0, 2, 1)),  # 16-byte 128x64 tiles: 3 slices, partial tiles
+    ((2, 4100, 4096), (0, 2, 1)),  # 16-byte 128x128 tiles (>= 8 per CU), partial last w-tile
+    ((130, 70), (1, 0)),         # H = 70 not a multiple of 4: the 4-byte tiles
     ((17,), (0,)),
 ])
 def test_permuted_views_bit_exact(cont, shape, perm):

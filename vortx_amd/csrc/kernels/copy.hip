@@ -6,7 +6,8 @@
 // row-major index. Indices are 64-bit here (the shader's u32 `it` wraps past
 // 2^32 elements).
 //
-// Three kernels, all HBM-bound (8 bytes of traffic per element):
+// Four kernels (one in two tile shapes), all HBM-bound (8 bytes of traffic
+// per element):
 //   vx_contiguous_gen  any strides; one element per lane per step, the
 //                      row-major index split with precomputed reciprocals;
 //                      reads are coalesced when s3 == 1;
@@ -15,7 +16,12 @@
 //   vx_contiguous_t64  views whose h axis is the contiguous one (s2 == 1,
 //                      e.g. a transposed matrix): 64 x 64 tiles through LDS
 //                      so that both the reads (along h) and the writes
-//                      (along w) are coalesced.
+//                      (along w) are coalesced;
+//   vx_contiguous_t128 the same views when 16-byte moves are aligned (H, W,
+//   (and _t128x64)     s0, s1, s3 multiples of 4, aligned bases): 128 x 128
+//                      (or 128 x 64) tiles, float4 reads along h and float4
+//                      writes along w (a quarter of the memory instructions,
+//                      512-byte segments), a grid-stride loop over tiles.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -100,4 +106,60 @@ extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t64(vx_copy_args
             }
         }
     }
+}
+
+// grid: a multiple of the CU count, looping over tiles (n c, h-band, w-band)
+// with w fastest. 256 threads; each phase moves the TH x TW tile as float4,
+// thread t taking float4 t + 256 i. LDS holds the tile as [w][h] with pitch
+// TH + 1 so the column reads of the write phase fall in different banks.
+template <uint32_t TH, uint32_t TW>
+__device__ __forceinline__ void vx_contiguous_tile16(const vx_copy_args& a) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    constexpr uint32_t P = TH + 1u, NV = TH * TW / 1024u, QH = TH / 4u, QW = TW / 4u;
+    __shared__ uint32_t tile[TW * P];
+    const uint32_t H = a.size[2], W = a.size[3], C = a.size[1];
+    const uint32_t tw_n = (W + TW - 1u) / TW, th_n = (H + TH - 1u) / TH;
+    const uint32_t per_nc = tw_n * th_n;
+    const uint32_t ntiles = per_nc * a.size[0] * C;  // < 2^32 (the host checks)
+    const uint32_t t = threadIdx.x;
+    for (uint32_t id = blockIdx.x; id < ntiles; id += gridDim.x) {
+        const uint32_t nc = id / per_nc, r = id - nc * per_nc;
+        const uint32_t th = r / tw_n, tw = r - th * tw_n;
+        const uint32_t h0 = th * TH, w0 = tw * TW;
+        const uint32_t n = nc / C, c = nc - n * C;
+        const uint32_t* sb = a.src + (int64_t)n * a.stride[0] + (int64_t)c * a.stride[1];
+        uint32_t* db = a.dst + (uint64_t)nc * H * W;
+        // read: float4 f = (column f / QH, rows 4 (f % QH) .. + 3)
+        u32x4 v[NV];
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            const uint32_t f = t + 256u * i;
+            const uint32_t h = h0 + 4u * (f % QH), w = w0 + f / QH;
+            v[i] = (h < H && w < W) ? *(const u32x4*)(sb + h + (int64_t)w * a.stride[3]) : u32x4{0u, 0u, 0u, 0u};
+        }
+        __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            const uint32_t f = t + 256u * i;
+            uint32_t* d = tile + (f / QH) * P + 4u * (f % QH);
+            d[0] = v[i].x; d[1] = v[i].y; d[2] = v[i].z; d[3] = v[i].w;
+        }
+        __syncthreads();
+        // write: float4 f = (row f / QW, columns 4 (f % QW) .. + 3)
+#pragma unroll
+        for (uint32_t i = 0; i < NV; ++i) {
+            const uint32_t f = t + 256u * i;
+            const uint32_t hl = f / QW, w4 = f % QW;
+            const uint32_t h = h0 + hl, w = w0 + 4u * w4;
+            const uint32_t* q = tile + 4u * w4 * P + hl;
+            if (h < H && w < W) *(u32x4*)(db + (uint64_t)h * W + w) = u32x4{q[0], q[P], q[2u * P], q[3u * P]};
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t128(vx_copy_args a) {
+    vx_contiguous_tile16<128u, 128u>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t128x64(vx_copy_args a) {
+    vx_contiguous_tile16<128u, 64u>(a);
 }

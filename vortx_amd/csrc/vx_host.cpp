@@ -676,6 +676,23 @@ static int run_contiguous(vx_ctx ctx, vx_stream stream, const vx_mview* out, con
     a.dc = make_udiv(c.size[1]);
     DeviceGuard guard(ctx->device);
     const bool tile = c.stride[2] == 1u && c.stride[3] != 1u && c.size[2] >= 16u && c.size[3] >= 16u;
+    // 16-byte tiles: every float4 of a row (along h in, along w out) aligned
+    // 128 x 128 tiles (66 KB of LDS, 2 workgroups per CU) when there are at
+    // least 8 per CU, else 128 (h) x 64 (w) tiles (33 KB, 4 per CU): 8192^2
+    // 4.73 vs 4.64 TB/s, 4096^2 4.27 vs 4.91 TB/s.
+    const uint64_t nbig = (uint64_t)((c.size[3] + 127u) / 128u) * ((c.size[2] + 127u) / 128u) * c.size[0] * c.size[1];
+    const bool big = nbig >= 8ull * (uint64_t)ctx->num_cus;
+    const uint64_t ntiles128 = big ? nbig
+                                   : (uint64_t)((c.size[3] + 63u) / 64u) * ((c.size[2] + 127u) / 128u) * c.size[0] *
+                                         c.size[1];
+    const bool tile16 = tile && !dev_offset && c.size[2] % 4u == 0u && c.size[3] % 4u == 0u &&
+                        c.stride[0] % 4 == 0 && c.stride[1] % 4 == 0 && c.stride[3] % 4 == 0 &&
+                        aligned16((uintptr_t)a.src) && aligned16((uintptr_t)a.dst) && ntiles128 < (1ull << 32);
+    if (tile16) {
+        const uint64_t maxb = (uint64_t)ctx->num_cus * 8u;
+        return launch(ctx, big ? K_vx_contiguous_t128 : K_vx_contiguous_t128x64,
+                      dim3((uint32_t)(ntiles128 < maxb ? ntiles128 : maxb)), dim3(256), 0, stream, a);
+    }
     if (tile) {
         auto cap = [](uint64_t v) { return (uint32_t)(v < 65535u ? v : 65535u); };
         return launch(ctx, K_vx_contiguous_t64, dim3(cap((c.size[3] + 63u) / 64u), cap((c.size[2] + 63u) / 64u),
