@@ -79,7 +79,9 @@ def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 @pytest.mark.parametrize("B", [1, 2, 3, 4, 8, 16, 21])
-@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536)])
+# (93, 832): 13 units of 64, so the batched kernel's last round is ragged
+# (Q4_K skips: K is not a multiple of 256); (1, 4096): a single row.
+@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536), (93, 832), (1, 4096)])
 def test_gemv_parity_small(qgemv, qtype, B, M, K):
     if K % O.QTYPE_INFO[qtype][0]:
         pytest.skip("K not a multiple of the block size")
