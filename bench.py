@@ -298,6 +298,7 @@ def cpu_baselines(threads: int):
     from vortx_amd import synthetic as S
 
     out = {}
+    bind = f"; OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND', 'unset')}"
     M, K = 11008, 4096
     w = S.quant_weights(O.Q4_0, M, K, seed=100).numpy()
     x = S.activations(1, K, seed=7).numpy()
@@ -309,7 +310,7 @@ def cpu_baselines(threads: int):
     dt = (time.perf_counter() - t0) / n
     out["q4_0"] = {"value": gemv_bytes(2, M, K, 1) / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
                    "sample": f"{n} x Q4_0 GEMV 11008x4096 b=1 on one 25 MB matrix (oracle gemv_q_f32_omp, "
-                             f"builder's dequant-dot restatement; the reference has no quantized path)"}
+                             f"builder's dequant-dot restatement; the reference has no quantized path){bind}"}
     a = np.random.default_rng(1).uniform(-1, 1, (1024, 1024)).astype(np.float32)
     b = np.random.default_rng(2).uniform(-1, 1, (1024, 1024)).astype(np.float32)
     for _ in range(3):  # examples/gemm_bench.rs:11-12: 3 warmup + 10 timed
@@ -320,7 +321,7 @@ def cpu_baselines(threads: int):
     dt = (time.perf_counter() - t0) / 10
     out["gemm1024"] = {"value": 2.0 * 1024 ** 3 / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
                        "sample": "10 timed (3 warmup) f32 GEMM 1024^3, OpenMP restatement of gemm_tiled "
-                                 "(64x64x16 tiles, reference k order)"}
+                                 f"(64x64x16 tiles, reference k order){bind}"}
     for M, N, K, key in ((4096, 4096, 4096, "gemm4096"), (4096, 11008, 4096, "gemm4096x11008")):
         a = np.random.default_rng(1).uniform(-1, 1, (M, K)).astype(np.float32)
         b = np.random.default_rng(2).uniform(-1, 1, (K, N)).astype(np.float32)
@@ -331,7 +332,7 @@ def cpu_baselines(threads: int):
         dt = (time.perf_counter() - t0) / 3
         out[key] = {"value": 2.0 * M * N * K / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
                     "sample": f"3 timed (1 warmup) f32 GEMM {M}x{N}x{K}, OpenMP restatement of gemm_tiled "
-                              f"(64x64x16 tiles, reference k order)"}
+                              f"(64x64x16 tiles, reference k order){bind}"}
     return out
 
 
@@ -347,6 +348,9 @@ def main() -> int:
               "(the hot path shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         return 2
 
+    # CPU baseline threads pinned close together; set before any OpenMP
+    # runtime starts (torch's, or the oracle library's when it loads)
+    os.environ.setdefault("OMP_PROC_BIND", "close")
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
