@@ -122,10 +122,10 @@ int vx_gguf_type_size(uint32_t ggml_type, uint32_t* block_elems, uint32_t* block
 
 /* Copies bytes [offset, offset + nbytes) of the data section into device
  * memory at `device_dst` (any device address of the context's device).
- * Up to 4 host threads each pread 16 MB chunks of the file into two pinned
- * staging buffers of their own (hipHostMalloc, allocated per call) and copy
- * them with hipMemcpyAsync on a stream of their own, so reading the file
- * overlaps the DMA. Those streams first wait for the work already queued
+ * Two host threads (VX_GGUF_UPLOAD_THREADS, 1..64, overrides) each pread
+ * 16 MB chunks of the file into two pinned staging buffers of their own
+ * (hipHostMalloc, allocated per call) and copy them with hipMemcpyAsync on a
+ * stream of their own, so reading the file overlaps the DMA. Those streams first wait for the work already queued
  * on `stream`; the call returns after every copy has completed and the
  * staging is freed. Uploading the whole data section once (offset 0,
  * nbytes = data_size) keeps every tensor at device_dst + tensor.offset
