@@ -118,6 +118,36 @@ __device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base
     }
 }
 
+// The same fragment for a tile that lies inside the operand along x and a
+// stage that lies inside K: every load unconditional (no zero fill), so the
+// compiler counts outstanding loads exactly across the pipelined loop.
+template <int MODE>
+__device__ __forceinline__ void vx_load_frag_full(vx_frag<MODE>& f, const float* base, int64_t sx, int64_t sk,
+                                                  uint32_t x0, uint32_t k0) {
+    const uint32_t t = threadIdx.x;
+    if constexpr (MODE == MODE_KC) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const f32x4 q = *(const f32x4*)(base + (int64_t)(x0 + (fi >> 2)) * sx + k0 + 4u * (fi & 3u));
+            f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
+        }
+    } else if constexpr (MODE == MODE_XC) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t fi = t + 256u * i;
+            const f32x4 q = *(const f32x4*)(base + (int64_t)(k0 + (fi >> 5)) * sk + x0 + 4u * (fi & 31u));
+            f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t fi = t + 256u * i;
+            f.v[i] = base[(int64_t)(k0 + (fi >> 7)) * sk + (int64_t)(x0 + (fi & 127u)) * sx];
+        }
+    }
+}
+
 // Register fragment -> LDS tile S[k][x] (row pitch LD).
 template <int MODE, int LD>
 __device__ __forceinline__ void vx_store_frag(const vx_frag<MODE>& f, float* S) {
@@ -183,25 +213,10 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    vx_frag<AMODE> fa;
-    vx_frag<BMODE> fb;
-    const uint32_t nk = (p.K + TBK - 1) / TBK;
-    if (nk) {
-        vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
-        vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
-        vx_store_frag<AMODE, LDA_S>(fa, As[0]);
-        vx_store_frag<BMODE, LDB_S>(fb, Bs[0]);
-        __syncthreads();
-    }
-    for (uint32_t kt = 0; kt < nk; ++kt) {
-        const uint32_t cur = kt & 1u;
-        const bool more = kt + 1 < nk;
-        if (more) {
-            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
-            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
-        }
-        const float* as = As[cur] + wm * 64u + l32;
-        const float* bs = Bs[cur] + wn * 64u + l32;
+    // One TBK stage from LDS buffer `buf`.
+    auto mma = [&](uint32_t buf) {
+        const float* as = As[buf] + wm * 64u + l32;
+        const float* bs = Bs[buf] + wn * 64u + l32;
 #pragma unroll
         for (int ks = 0; ks < TBK / 2; ++ks) {
             const uint32_t kk = 2u * ks + lk;
@@ -212,11 +227,87 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
             acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
             acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
         }
-        if (more) {
-            vx_store_frag<AMODE, LDA_S>(fa, As[cur ^ 1u]);
-            vx_store_frag<BMODE, LDB_S>(fb, Bs[cur ^ 1u]);
+    };
+
+    const uint32_t nkf = p.K / TBK;  // whole stages
+    if (m0 + TBM <= p.M && n0 + TBN <= p.N) {
+        // Tile inside M and N: the loads for stage s + 2 are issued while
+        // stage s is multiplied (two register buffers), so each load has two
+        // stages of MFMAs to arrive before its LDS store waits for it. Stage
+        // indices are clamped to the last whole stage (the extra loads at the
+        // end are harmless). Unrolled by two so each buffer is named.
+        if (nkf) {
+            vx_frag<AMODE> ra0, ra1;
+            vx_frag<BMODE> rb0, rb1;
+            auto ld = [&](uint32_t st, vx_frag<AMODE>& fa_, vx_frag<BMODE>& fb_) {
+                const uint32_t k0 = min(st, nkf - 1u) * TBK;
+                vx_load_frag_full<AMODE>(fa_, A, p.as[2], p.as[3], m0, k0);
+                vx_load_frag_full<BMODE>(fb_, B, p.bs[3], p.bs[2], n0, k0);
+            };
+            ld(0u, ra0, rb0);
+            ld(1u, ra1, rb1);
+            vx_store_frag<AMODE, LDA_S>(ra0, As[0]);
+            vx_store_frag<BMODE, LDB_S>(rb0, Bs[0]);
+            __syncthreads();
+            // Invariant at the top: stage st in buffer 0, stage st + 1 in
+            // flight to ra1 / rb1.
+            uint32_t st = 0;
+            for (; st + 2u <= nkf; st += 2u) {
+                ld(st + 2u, ra0, rb0);
+                // keep the loads above the MFMAs (the scheduler would sink them
+                // below the other buffer's store and share its registers)
+                __builtin_amdgcn_sched_barrier(0);
+                mma(0u);
+                vx_store_frag<AMODE, LDA_S>(ra1, As[1]);
+                vx_store_frag<BMODE, LDB_S>(rb1, Bs[1]);
+                __syncthreads();
+                ld(st + 3u, ra1, rb1);
+                __builtin_amdgcn_sched_barrier(0);
+                mma(1u);
+                vx_store_frag<AMODE, LDA_S>(ra0, As[0]);
+                vx_store_frag<BMODE, LDB_S>(rb0, Bs[0]);
+                __syncthreads();
+            }
+            if (st < nkf) mma(0u);  // an odd stage count: the last one
         }
-        __syncthreads();
+        if (p.K % TBK) {
+            // the K tail: one stage zero-filled past K, through buffer 1
+            // (its last reader finished before a barrier)
+            vx_frag<AMODE> fa;
+            vx_frag<BMODE> fb;
+            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, nkf * TBK, p.K);
+            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, nkf * TBK, p.K);
+            vx_store_frag<AMODE, LDA_S>(fa, As[1]);
+            vx_store_frag<BMODE, LDB_S>(fb, Bs[1]);
+            __syncthreads();
+            mma(1u);
+        }
+    } else {
+        // Edge tile: zero-filled loads of the next stage during this one.
+        vx_frag<AMODE> fa;
+        vx_frag<BMODE> fb;
+        const uint32_t nk = (p.K + TBK - 1) / TBK;
+        if (nk) {
+            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
+            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
+            vx_store_frag<AMODE, LDA_S>(fa, As[0]);
+            vx_store_frag<BMODE, LDB_S>(fb, Bs[0]);
+            __syncthreads();
+        }
+        for (uint32_t kt = 0; kt < nk; ++kt) {
+            const uint32_t cur = kt & 1u;
+            const bool more = kt + 1 < nk;
+            if (more) {
+                vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
+                vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
+            }
+            mma(cur);
+            if (more) {
+                vx_store_frag<AMODE, LDA_S>(fa, As[cur ^ 1u]);
+                vx_store_frag<BMODE, LDB_S>(fb, Bs[cur ^ 1u]);
+            }
+            __syncthreads();
+        }
     }
 
     // D layout of v_mfma_f32_32x32x2f32: register v of lane l holds
