@@ -336,21 +336,35 @@ def cpu_baselines(threads: int):
     return out
 
 
+def cpu_baselines_child(threads: int):
+    """cpu_baselines in a child process of its own (no GPU use there), with
+    its OpenMP threads pinned close together (OMP_PROC_BIND=close): pinning
+    in this process would bind the main thread, and with it the GGUF upload's
+    reader threads, to one core."""
+    import subprocess
+    env = dict(os.environ, OMP_PROC_BIND=os.environ.get("OMP_PROC_BIND", "close"), OMP_NUM_THREADS=str(threads))
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-only", str(threads)], env=env,
+                       stdout=subprocess.PIPE, check=True, text=True)
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-baseline-only", type=int, default=0, metavar="THREADS",
+                    help=argparse.SUPPRESS)  # the CPU leg's own process: print its JSON and exit
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the hot path shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         return 2
 
-    # CPU baseline threads pinned close together; set before any OpenMP
-    # runtime starts (torch's, or the oracle library's when it loads)
-    os.environ.setdefault("OMP_PROC_BIND", "close")
+    if args.cpu_baseline_only:
+        print(json.dumps(cpu_baselines(args.cpu_baseline_only)), flush=True)
+        return 0
     import torch
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -398,7 +412,7 @@ def main() -> int:
     log(f"[gguf_upload] {gg}")
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
-    cpu = None if args.no_cpu else cpu_baselines(threads)
+    cpu = None if args.no_cpu else cpu_baselines_child(threads)
     if cpu:
         log(f"[cpu] {cpu}")
 
