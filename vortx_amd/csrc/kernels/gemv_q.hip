@@ -890,7 +890,8 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     const uint32_t nitems = nts * upw;
 
     // LDS: xq [col][unit][2][64] int8 | scl [col][unit] {c2_0, S_0, c2_1,
-    // S_1} | red [slot][16 waves][col][16] | 64 zero bytes at a.upitch.
+    // S_1} (S = sum of the block's x; -8 times that for Q4_0) | red [slot]
+    // [16 waves][col][16] | 64 zero bytes at a.upitch.
     uint8_t* xq = (uint8_t*)vx_lds_x;
     f32x4* scl = (f32x4*)(xq + 128u * B * nunits);
     float* red = (float*)(scl + B * nunits);
@@ -979,7 +980,9 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
         xu[1] = uint4{l0[4], l0[5], l0[6], l0[7]};
         xu[4] = uint4{l1[0], l1[1], l1[2], l1[3]};
         xu[5] = uint4{l1[4], l1[5], l1[6], l1[7]};
-        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m + ps, ps};  // non-finite x: into y
+        // Q4_0 keeps -8 sum(x): its block offset is then folded into one FMA
+        const float so_x = QT == VX_Q4_0 ? -8.f * ps : ps;
+        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m + ps, so_x};  // non-finite x: into y
     };
     if (t < nblk) split(t, xr);
     for (uint32_t g = t + VX_B_WG; g < nblk; g += VX_B_WG) {
@@ -1047,11 +1050,18 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
                         if (col < B) {
                             const f32x4 sc = scl[col * nunits + u];
                             float v = acc[2 * cp + c];
-                            v = __builtin_fmaf(st[0], sc.x * tq[cp][c][0], v);
-                            v = __builtin_fmaf(st[1], sc.z * tq[cp][c][1], v);
-                            if constexpr (QT != VX_Q8_0) {
-                                v = __builtin_fmaf(so[0], sc.y, v);
-                                v = __builtin_fmaf(so[1], sc.w, v);
+                            if constexpr (QT == VX_Q4_0) {
+                                // d (c2 T - 8 sum x): the block scale times its int dot
+                                // minus the offset of the biased nibbles
+                                v = __builtin_fmaf(st[0], __builtin_fmaf(sc.x, tq[cp][c][0], sc.y), v);
+                                v = __builtin_fmaf(st[1], __builtin_fmaf(sc.z, tq[cp][c][1], sc.w), v);
+                            } else {
+                                v = __builtin_fmaf(st[0], sc.x * tq[cp][c][0], v);
+                                v = __builtin_fmaf(st[1], sc.z * tq[cp][c][1], v);
+                                if constexpr (QT != VX_Q8_0) {
+                                    v = __builtin_fmaf(so[0], sc.y, v);
+                                    v = __builtin_fmaf(so[1], sc.w, v);
+                                }
                             }
                             acc[2 * cp + c] = v;
                         }
