@@ -137,3 +137,34 @@ def test_quantize_errors(qgemv):
     with pytest.raises(vx.VortxError) as e:
         qgemv.quantize(vx.QWeight(out, vx.VX_Q8_0, 8, 64), x.reshape(-1))
     assert e.value.status == vx._ffi.VX_ERR_SHAPE
+
+
+@pytest.mark.parametrize("qtype", [vx.VX_Q8_0, vx.VX_Q4_0], ids=lambda q: QN[q])
+@pytest.mark.parametrize("layout", ["padded-rows", "unaligned-base"])
+def test_quantize_output_layouts(qgemv, qtype, layout):
+    """Rows padded past their blocks take per-block stores; dense rows are
+    staged and copied out, with 2-byte stores when the output base is not
+    16-byte aligned. Bytes equal the oracle's and nothing outside the blocks
+    is written."""
+    rng = np.random.default_rng(45)
+    M, K = 45, 1024
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    rb = S.row_bytes(qtype, K)
+    note(f"quantize {QN[qtype]} {layout}")
+    if layout == "padded-rows":
+        buf = torch.full((M, rb + 6), 0xAB, dtype=torch.uint8, device=DEV)
+        qw = vx.QWeight(buf, qtype, M, K, row_stride=rb + 6)
+    else:
+        flat = torch.full((M * rb + 16,), 0xAB, dtype=torch.uint8, device=DEV)
+        buf = flat[2:2 + M * rb].view(M, rb)
+        qw = vx.QWeight(buf, qtype, M, K)
+    qgemv.quantize(qw, torch.from_numpy(x).to(DEV))
+    torch.cuda.synchronize()
+    ref = O.quantize(qtype, x)
+    got = buf.cpu().numpy()
+    assert np.array_equal(got[:, :rb], ref)
+    if layout == "padded-rows":
+        assert (got[:, rb:] == 0xAB).all(), "wrote into the row padding"
+    else:
+        f = flat.cpu().numpy()
+        assert (f[:2] == 0xAB).all() and (f[2 + M * rb:] == 0xAB).all(), "wrote outside the output"

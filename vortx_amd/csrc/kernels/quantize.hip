@@ -8,7 +8,8 @@
 // sequential CPU run of the same algorithm bit for bit. The reference
 // (vortx) has no quantized code; this is the step before its GEMV.
 //
-//   vx_quantize_q8_0 / _q4_0  one lane per 32-block (HBM-bound);
+//   vx_quantize_q8_0 / _q4_0  one lane per 32-block (HBM-bound; Q8_0's
+//                             blocks staged in LDS for 16-byte stores);
 //   vx_quantize_q4_k          8 lanes per 256-super-block, lane j running
 //                             the scale/min search of sub-block j, the
 //                             lanes meeting through shuffles for the
@@ -55,64 +56,123 @@ __device__ __forceinline__ void vx_q_load32(const vx_quant_args& a, uint32_t row
     }
 }
 
-// grid: x covers the blocks of a row (256 per workgroup), y the rows (loop).
-extern "C" __global__ __launch_bounds__(256) void vx_quantize_q8_0(vx_quant_args a) {
-    const uint32_t b = blockIdx.x * 256u + threadIdx.x;
-    if (b >= a.nblk) return;
-    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
-        float x[32];
-        vx_q_load32(a, row, 32u * b, x);
-        float amax = 0.0f;
+// One Q8_0 block (quantize_row_q8_0_ref): 17 little-endian u16 words, the
+// f16 scale then the 32 int8 values in pairs.
+__device__ __forceinline__ void vx_q8_0_block(const float (&x)[32], uint16_t (&w)[17]) {
+    float amax = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            const float v = fabsf(x[j]);
-            amax = amax > v ? amax : v;
+    for (int j = 0; j < 32; ++j) {
+        const float v = fabsf(x[j]);
+        amax = amax > v ? amax : v;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    w[0] = vx_f32_to_f16_bits(d);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t q0 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j] * id);
+        const uint32_t q1 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j + 1] * id);
+        w[1 + j] = (uint16_t)(q0 | (q1 << 8));
+    }
+}
+
+// One Q4_0 block (quantize_row_q4_0_ref): 9 u16 words, the f16 scale then
+// the 16 bytes of nibble pairs (element j low, element j + 16 high).
+__device__ __forceinline__ void vx_q4_0_block(const float (&x)[32], uint16_t (&w)[9]) {
+    float amax = 0.0f, mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            mx = x[j];
         }
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint16_t* y = (uint16_t*)(a.out + (uint64_t)row * a.row_stride + 34ull * b);
-        y[0] = vx_f32_to_f16_bits(d);
+    }
+    const float d = mx / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    w[0] = vx_f32_to_f16_bits(d);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint32_t q0 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j] * id);
-            const uint32_t q1 = (uint32_t)(uint8_t)(int8_t)(int)__builtin_roundf(x[2 * j + 1] * id);
-            y[1 + j] = (uint16_t)(q0 | (q1 << 8));
+    for (int j = 0; j < 8; ++j) {
+        uint32_t pr = 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int jj = 2 * j + t;
+            int xi0 = (int8_t)(x[jj] * id + 8.5f);
+            int xi1 = (int8_t)(x[16 + jj] * id + 8.5f);
+            xi0 = xi0 < 15 ? xi0 : 15;
+            xi1 = xi1 < 15 ? xi1 : 15;
+            pr |= (uint32_t)(xi0 | (xi1 << 4)) << (8 * t);
+        }
+        w[1 + j] = (uint16_t)pr;
+    }
+}
+
+// Q8_0: thread t of each round takes block g0 + t of the flattened (row,
+// block) sequence (grid-stride over rounds of 256 blocks). With dense rows
+// (row stride = nblk blocks) a round's output is one contiguous range: it is
+// staged in LDS and written with 16-byte stores, which beats per-lane
+// 2-byte stores at a 34-byte lane stride (14336 x 4096: 60.4 -> 54.1 us).
+// Padded rows take the 2-byte stores. (Q4_0's 18-byte blocks measured
+// faster with its own row-per-workgroup kernel below, staged or not.)
+template <int NW>
+__device__ __forceinline__ void vx_quantize_blocks(const vx_quant_args& a) {
+    __shared__ uint4 stage[(256u * 2u * NW + 15u) / 16u];
+    uint16_t* st = (uint16_t*)stage;
+    const uint64_t G = (uint64_t)a.M * a.nblk;
+    const bool dense = a.row_stride == 2ull * NW * a.nblk;  // uniform
+    const bool out16 = (reinterpret_cast<uintptr_t>(a.out) & 15u) == 0u;
+    const uint32_t t = threadIdx.x;
+    for (uint64_t g0 = (uint64_t)blockIdx.x * 256u; g0 < G; g0 += (uint64_t)gridDim.x * 256u) {
+        const uint64_t g = g0 + t;
+        if (g < G) {
+            const uint32_t row = (uint32_t)(g / a.nblk), b = (uint32_t)(g - (uint64_t)row * a.nblk);
+            float x[32];
+            vx_q_load32(a, row, 32u * b, x);
+            uint16_t w[NW];
+            if constexpr (NW == 17) vx_q8_0_block(x, w);
+            else vx_q4_0_block(x, w);
+            if (dense) {
+#pragma unroll
+                for (int j = 0; j < NW; ++j) st[NW * t + j] = w[j];
+            } else {
+                uint16_t* y = (uint16_t*)(a.out + (uint64_t)row * a.row_stride + 2ull * NW * b);
+#pragma unroll
+                for (int j = 0; j < NW; ++j) y[j] = w[j];
+            }
+        }
+        if (dense) {
+            __syncthreads();
+            const uint32_t nb = G - g0 < 256u ? (uint32_t)(G - g0) : 256u;
+            const uint32_t nh = NW * nb;             // u16 words of this round
+            uint8_t* dst = a.out + g0 * 2u * NW;     // 16-byte aligned when out is: 256 blocks = 16 * (32 NW) bytes
+            uint32_t done = 0;
+            if (out16) {
+                const uint32_t n16 = nh / 8u;
+                for (uint32_t i = t; i < n16; i += 256u) ((uint4*)dst)[i] = stage[i];
+                done = 8u * n16;
+            }
+            for (uint32_t i = done + t; i < nh; i += 256u) ((uint16_t*)dst)[i] = st[i];
+            __syncthreads();  // the next round rewrites the stage
         }
     }
 }
 
+// grid: a multiple of the CU count; 256 threads, one 32-block each per round.
+extern "C" __global__ __launch_bounds__(256) void vx_quantize_q8_0(vx_quant_args a) {
+    vx_quantize_blocks<17>(a);
+}
+
+// grid: x covers the blocks of a row (256 per workgroup), y the rows (loop).
 extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_0(vx_quant_args a) {
     const uint32_t b = blockIdx.x * 256u + threadIdx.x;
     if (b >= a.nblk) return;
     for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
         float x[32];
         vx_q_load32(a, row, 32u * b, x);
-        float amax = 0.0f, mx = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-            if (amax < fabsf(x[j])) {
-                amax = fabsf(x[j]);
-                mx = x[j];
-            }
-        }
-        const float d = mx / -8.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint16_t w[9];
+        vx_q4_0_block(x, w);
         uint16_t* y = (uint16_t*)(a.out + (uint64_t)row * a.row_stride + 18ull * b);
-        y[0] = vx_f32_to_f16_bits(d);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            uint32_t pr = 0;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int jj = 2 * j + t;
-                int xi0 = (int8_t)(x[jj] * id + 8.5f);
-                int xi1 = (int8_t)(x[16 + jj] * id + 8.5f);
-                xi0 = xi0 < 15 ? xi0 : 15;
-                xi1 = xi1 < 15 ? xi1 : 15;
-                pr |= (uint32_t)(xi0 | (xi1 << 4)) << (8 * t);
-            }
-            y[1 + j] = (uint16_t)pr;
-        }
+        for (int j = 0; j < 9; ++j) y[j] = w[j];
     }
 }
 

@@ -743,9 +743,15 @@ static int run_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, con
         if (blocks > maxb) blocks = maxb;
         return launch(ctx, K_vx_quantize_q4_k, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
     }
+    if (out->qtype == VX_Q8_0) {
+        // rounds of 256 blocks of the flattened (row, block) sequence, grid-stride
+        uint64_t blocks = ((uint64_t)a.M * a.nblk + 255u) / 256u;
+        const uint64_t maxb = (uint64_t)ctx->num_cus * 16u;
+        if (blocks > maxb) blocks = maxb;
+        return launch(ctx, K_vx_quantize_q8_0, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+    }
     const uint32_t gy = a.M < 65535u ? a.M : 65535u;
-    return launch(ctx, out->qtype == VX_Q8_0 ? K_vx_quantize_q8_0 : K_vx_quantize_q4_0, dim3((a.nblk + 255u) / 256u, gy),
-                  dim3(256), 0, stream, a);
+    return launch(ctx, K_vx_quantize_q4_0, dim3((a.nblk + 255u) / 256u, gy), dim3(256), 0, stream, a);
 }
 
 static int run_dequant(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
