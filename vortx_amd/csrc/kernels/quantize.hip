@@ -182,6 +182,16 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_0(vx_quant_args
 // Instead of copying the winning candidate's levels on each improvement, the
 // (iscale, min) pair that produced them is kept and the levels are rebuilt
 // once by vx_qkx2_levels: the same nearest_int(iscale * (x - min)), clamped.
+// (float) MAX(0, MIN(15, nearest_int(v))) of make_qkx2_quants' search for
+// |v| < 2^22 (ggml's nearest_int asserts |v| <= 4194303): there its
+// 1.5 * 2^23 magic rounds to nearest even exactly like v_rndne_f32, and
+// v_med3_f32 clamps in float, so no integer round trip. The only
+// difference, a -0 level for v in (-0.5, -0], changes none of the sums or
+// squared differences it enters.
+__device__ __forceinline__ float vx_level(float v) {
+    return __builtin_amdgcn_fmed3f(__builtin_rintf(v), 0.f, 15.f);
+}
+
 struct vx_qkx2_best {
     float iscale, mnu;  // the winning candidate's inputs; iscale 0 = all levels 0
 };
@@ -215,8 +225,7 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
     best.mnu = mn;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const int l = vx_nearest_int(iscale * (x[i] - mn));
-        const float fl = (float)(l < 0 ? 0 : l > nmax ? nmax : l);
+        const float fl = vx_level(iscale * (x[i] - mn));
         float diff = scale * fl + mn - x[i];
         diff = diff * diff;
         best_mad += w[i] * diff;
@@ -227,9 +236,7 @@ __device__ __forceinline__ float vx_make_qkx2(const float (&x)[32], const float 
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            int l = vx_nearest_int(iscale * (x[i] - mn));
-            l = l < 0 ? 0 : l > nmax ? nmax : l;
-            fl[i] = (float)l;
+            fl[i] = vx_level(iscale * (x[i] - mn));
             sum_l += w[i] * fl[i];
             sum_l2 += w[i] * fl[i] * fl[i];
             sum_xl += w[i] * fl[i] * x[i];
