@@ -326,11 +326,12 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
         }
 }
 
-// WPE 4 (amdgpu_waves_per_eu(4, 4)) caps a kernel at 128 registers (the
-// vector modes need ~109, accumulators in VGPRs instead of 140 with AGPRs):
-// four 256-thread workgroups per CU (LDS 4 x 33 KB), so a 4096^3 problem
-// (1024 tiles) is resident at once instead of 768 tiles plus a tail at a
-// third occupancy. The all-scalar mode would spill under the cap (WPE 1).
+// WPE 3 (amdgpu_waves_per_eu(3, 4)) caps a kernel at 168 registers: three
+// 256-thread workgroups per CU. The two-stage prefetch's second register
+// buffer needs ~150-166 registers; squeezed into WPE 4's 128 (four
+// workgroups per CU) it ran slower: 4096^3 118.7 vs 123.5 TFLOP/s, B
+// transposed 126.4 vs 134.9, 1024^3 25.5 vs 29.8 (same-box A/B). The
+// all-scalar mode needs more and is left uncapped (WPE 1).
 #define VX_GEMM_MFMA(AM, BM, NAME, WPE)                                                              \
     extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(WPE, 4)))    \
     void vx_gemm_mfma_##NAME(vx_gemm_args p) {                                                       \
@@ -338,13 +339,13 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     }
 // Suffix letters: A mode then B mode; k = contiguous along K,
 // x = contiguous along M / N, g = generic.
-VX_GEMM_MFMA(MODE_KC, MODE_XC, kx, 4)  // row-major A, row-major B
-VX_GEMM_MFMA(MODE_KC, MODE_KC, kk, 4)  // row-major A, B = transposed view of [N, K]
-VX_GEMM_MFMA(MODE_XC, MODE_XC, xx, 4)
-VX_GEMM_MFMA(MODE_XC, MODE_KC, xk, 4)
+VX_GEMM_MFMA(MODE_KC, MODE_XC, kx, 3)  // row-major A, row-major B
+VX_GEMM_MFMA(MODE_KC, MODE_KC, kk, 3)  // row-major A, B = transposed view of [N, K]
+VX_GEMM_MFMA(MODE_XC, MODE_XC, xx, 3)
+VX_GEMM_MFMA(MODE_XC, MODE_KC, xk, 3)
 VX_GEMM_MFMA(MODE_GEN, MODE_GEN, gg, 1)
-VX_GEMM_MFMA(MODE_KC, MODE_GEN, kg, 4)
-VX_GEMM_MFMA(MODE_GEN, MODE_XC, gx, 4)
+VX_GEMM_MFMA(MODE_KC, MODE_GEN, kg, 3)
+VX_GEMM_MFMA(MODE_GEN, MODE_XC, gx, 3)
 
 // ---------------------------------------------------------------- gemv
 // y[m] = sum_k A[m, k] x[k]; A contiguous along K with 16-byte aligned
