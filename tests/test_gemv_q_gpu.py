@@ -286,3 +286,31 @@ def test_non_finite_x_reaches_its_column_only(qgemv, qtype, B, bad):
     assert not torch.isfinite(y[0]).any(), "a non-finite x value was lost"
     if B > 1:
         assert torch.equal(y[1:].view(torch.int32), y0[1:].view(torch.int32))
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("path", ["k-large", "rows", "rows-f32", "x-f32", "simt"])
+@pytest.mark.parametrize("bad", [float("nan"), float("inf")], ids=["nan", "inf"])
+def test_non_finite_x_other_paths(qgemv, qtype, path, bad, monkeypatch):
+    """The same on the other routes: batch 1 with K > 16384 (the per-row-group
+    int8 kernels by default), VX_GEMV_B1=rows with int8 or f32 x, f32 x at
+    batch 1 (VX_GEMV_X_F32) and the exact-f32 batched kernels
+    (VX_GEMV_BATCHED=simt)."""
+    M = 96
+    K = 16640 if path == "k-large" else 2048
+    B = 3 if path == "simt" else 1
+    if path in ("rows", "rows-f32"):
+        monkeypatch.setenv("VX_GEMV_B1", "rows")
+    if path == "simt":
+        monkeypatch.setenv("VX_GEMV_BATCHED", "simt")
+    x_f32 = path in ("rows-f32", "x-f32")
+    note(f"gemv non-finite x {QN[qtype]} path={path} {bad}")
+    w = vx.QWeight(S.quant_weights(qtype, M, K, seed=5, device=DEV), qtype, M, K)
+    x = S.activations(B, K, seed=6, device=DEV)
+    x[0, K - 5] = bad
+    y = torch.empty((B, M), device=DEV)
+    qgemv.dispatch(y.t(), w, x.t(), x_f32=x_f32)
+    torch.cuda.synchronize()
+    assert not torch.isfinite(y[0]).any(), "a non-finite x value was lost"
+    if B > 1:
+        assert torch.isfinite(y[1:]).all()

@@ -313,7 +313,8 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
 // and contributes d * c * T (minus the format's zero-point / min term).
 // LDS per chunk and batch column: x1 / x2 as [level][4 slots of 16 B][unit]
 // (odd unit pitch), then per 32-block: c, sum(x) (f32) and
-// O = sum(254 x1 + x2) (int32), indexed 2 * unit + half.
+// -8 O with O = sum(254 x1 + x2) (int32: Q4_0's zero point -8 sum(x) at the
+// scale c), indexed 2 * unit + half.
 struct vx_i8lds {
     uint32_t upitch, cu;
     __device__ __forceinline__ int4* x8(uint32_t b) const {
@@ -366,6 +367,9 @@ __device__ __forceinline__ void vx_stage_store_i8(const vx_gemv_args& a, uint32_
             sx += __shfl_xor(sx, off, 64);
             oz += __shfl_xor(oz, off, 64);
         }
+        // a non-finite block (fmaxf skips NaN; the sum does not) stores
+        // max + sum as its scale, so y is non-finite
+        const bool fin = m < __builtin_inff() && sx == sx;
         if (f < total) {
             const uint32_t b = NB == 1 ? 0u : f / per_col;
             const uint32_t rem = f - b * per_col;
@@ -376,9 +380,9 @@ __device__ __forceinline__ void vx_stage_store_i8(const vx_gemv_args& a, uint32_
             x8[((1u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
             if ((j & 7u) == 0) {
                 const uint32_t idx = 2u * ul + (j >> 3);
-                L.cs(NB, b)[idx] = c;
+                L.cs(NB, b)[idx] = fin ? c : m + sx;
                 L.sx(NB, b)[idx] = sx;
-                L.oz(NB, b)[idx] = oz;
+                L.oz(NB, b)[idx] = -8 * oz;
             }
         }
     }
@@ -409,7 +413,7 @@ __device__ __forceinline__ float vx_unit_dot_i8(const uint32_t (&r)[vx_unit<QT>:
         float res = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            int i1 = 0, i2 = 0;
+            int i1 = 0, i2 = ozb[h];  // the zero point -8 O starts the level-2 sum
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t lo = vx_and(q[4 * h + i], 0x0F0F0F0Fu);
@@ -419,7 +423,7 @@ __device__ __forceinline__ float vx_unit_dot_i8(const uint32_t (&r)[vx_unit<QT>:
                 i2 = __builtin_amdgcn_sdot4((int)lo, (int)x2[8 * h + i], i2, false);
                 i2 = __builtin_amdgcn_sdot4((int)hi, (int)x2[8 * h + 4 + i], i2, false);
             }
-            const int t = 254 * i1 + i2 - 8 * ozb[h];
+            const int t = __mul24(i1, 254) + i2;
             const float d = vx_f16_to_f32(h ? (r[4] >> 16) : r[0]);
             res = __builtin_fmaf(d * cb[h], (float)t, res);
         }
@@ -435,7 +439,7 @@ __device__ __forceinline__ float vx_unit_dot_i8(const uint32_t (&r)[vx_unit<QT>:
                 i1 = __builtin_amdgcn_sdot4((int)qd, (int)x1[8 * h + i], i1, false);
                 i2 = __builtin_amdgcn_sdot4((int)qd, (int)x2[8 * h + i], i2, false);
             }
-            const int t = 254 * i1 + i2;
+            const int t = __mul24(i1, 254) + i2;
             const float d = vx_f16_to_f32(h ? (r[8] >> 16) : r[0]);
             res = __builtin_fmaf(d * cb[h], (float)t, res);
         }
@@ -455,7 +459,7 @@ __device__ __forceinline__ float vx_unit_dot_i8(const uint32_t (&r)[vx_unit<QT>:
             b1 = __builtin_amdgcn_sdot4((int)hi, (int)x1[8 + i], b1, false);
             b2 = __builtin_amdgcn_sdot4((int)hi, (int)x2[8 + i], b2, false);
         }
-        const float t0 = (float)(254 * a1 + a2), t1 = (float)(254 * b1 + b2);
+        const float t0 = (float)(__mul24(a1, 254) + a2), t1 = (float)(__mul24(b1, 254) + b2);
         float res = __builtin_fmaf(d * (float)sc0 * cb[0], t0, -(dmin * (float)m0) * sxb[0]);
         res = __builtin_fmaf(d * (float)sc1 * cb[1], t1, res);
         return __builtin_fmaf(-(dmin * (float)m1), sxb[1], res);
@@ -548,7 +552,8 @@ __device__ __forceinline__ void vx_gemv_i8b1(const vx_gemv_args& a) {
 template <int QT, int P, int WGT, bool XV>
 __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
-    constexpr int XPT = (int)(VX_P_XF / WGT);
+    constexpr uint32_t XW = WGT < 512 ? WGT : 512u;
+    constexpr int XPT = (int)(VX_P_XF / XW);
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t nwv = gridDim.x * (WGT / 64u);
@@ -560,12 +565,16 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
 
     // 1. x loads (float4 f = slot f & 15 of unit f >> 4), then the bare
     //    barrier that puts them ahead of every weight request of the CU.
+    //    Only the first XW threads load and split x (two float4 each at
+    //    K = 4096): the requests leave as soon as the first waves of the CU
+    //    start, and the later waves only meet the barriers (1-6 % faster
+    //    than all 16 waves loading; 4 waves loading is slower).
     const uint32_t total = nunits * 16u;
     f32x4 xr[XPT];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-        if ((uint32_t)i * WGT >= total) break;  // uniform: rounds past x
-        const uint32_t f = min(t + WGT * (uint32_t)i, total - 1u);
+        if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;  // uniform: rounds past x
+        const uint32_t f = min(t + XW * (uint32_t)i, total - 1u);
         if constexpr (XV) {
             xr[i] = *(const f32x4*)(a.x + 4 * (int64_t)f);
         } else {
@@ -592,15 +601,16 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     for (int j = 0; j < PRE; ++j) {
         uint32_t u;
         const uint8_t* rp = item_ptr((uint32_t)j, u);
-        vx_load_unit<QT>(rp, u, wr[j]);
+        vx_load_unit<QT, true>(rp, u, wr[j]);
     }
 
     // 3. split x into the two levels and store them with the block scale c,
-    //    sum(x) and O = sum(254 x1 + x2) (|O| < 2^21: exact as a float sum).
+    //    sum(x) and -8 O, O = sum(254 x1 + x2) (|O| < 2^21: exact as a float
+    //    sum).
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-        if ((uint32_t)i * WGT >= total) break;
-        const uint32_t f = t + WGT * (uint32_t)i;
+        if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
+        const uint32_t f = t + XW * (uint32_t)i;
         const bool in = f < total;
         const f32x4 v = in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f};
         const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -629,7 +639,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
                 const uint32_t idx = 2u * ul + (j >> 3);
                 L.cs(1, 0)[idx] = fin ? c : m + sx;
                 L.sx(1, 0)[idx] = sx;
-                L.oz(1, 0)[idx] = (int)oz;
+                L.oz(1, 0)[idx] = -8 * (int)oz;
             }
         }
     }
@@ -641,7 +651,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     for (int j = PRE; j < P; ++j) {
         uint32_t u;
         const uint8_t* rp = item_ptr((uint32_t)j, u);
-        vx_load_unit<QT>(rp, u, wr[j]);
+        vx_load_unit<QT, true>(rp, u, wr[j]);
     }
     uint32_t x1[16], x2[16];
     float cb[2], sxb[2];
@@ -667,7 +677,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         acc += act ? d : 0.f;
         uint32_t nu;
         const uint8_t* rp = item_ptr(it + P, nu);
-        vx_load_unit<QT>(rp, nu, w);
+        vx_load_unit<QT, true>(rp, nu, w);
         if (p == npass - 1u) {
             const float sum = vx_wave_sum(acc);
             if (lane == 0) a.y[(int64_t)(gw + ri * nwv) * a.ys_m] = sum;

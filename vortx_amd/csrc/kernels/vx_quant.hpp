@@ -90,17 +90,19 @@ template <> struct vx_unit<VX_Q4_0> { static constexpr int NW = 9;  static const
 template <> struct vx_unit<VX_Q8_0> { static constexpr int NW = 17; static constexpr int QK = 32;  static constexpr int BB = 34; };
 template <> struct vx_unit<VX_Q4_K> { static constexpr int NW = 12; static constexpr int QK = 256; static constexpr int BB = 144; };
 
-// Raw bytes of unit u of a row into registers (row 4-byte aligned).
-template <int QT>
+// Raw bytes of unit u of a row into registers (row 4-byte aligned). With
+// U24 the caller guarantees u < 2^24, so the byte offset is a full-rate
+// 24-bit multiply instead of v_mul_lo_u32.
+template <int QT, bool U24 = false>
 __device__ __forceinline__ void vx_load_unit(const uint8_t* row, uint32_t u, uint32_t (&r)[vx_unit<QT>::NW]) {
     if constexpr (QT == VX_Q4_0) {
-        const uint8_t* p = row + 36u * u;
+        const uint8_t* p = row + (U24 ? __umul24(u, 36u) : 36u * u);
         u32x4_a4 a = vx_ld16(p), b = vx_ld16(p + 16);
         r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
         r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
         r[8] = vx_ld4(p + 32);
     } else if constexpr (QT == VX_Q8_0) {
-        const uint8_t* p = row + 68u * u;
+        const uint8_t* p = row + (U24 ? __umul24(u, 68u) : 68u * u);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             u32x4_a4 a = vx_ld16(p + 16 * i);
@@ -108,7 +110,7 @@ __device__ __forceinline__ void vx_load_unit(const uint8_t* row, uint32_t u, uin
         }
         r[16] = vx_ld4(p + 64);
     } else {
-        const uint8_t* sb = row + 144u * (u >> 2);
+        const uint8_t* sb = row + (U24 ? __umul24(u >> 2, 144u) : 144u * (u >> 2));
         const uint8_t* qs = sb + 16 + 32u * (u & 3u);
         u32x4_a4 h = vx_ld16(sb), a = vx_ld16(qs), b = vx_ld16(qs + 16);
         r[0] = h.x; r[1] = h.y; r[2] = h.z; r[3] = h.w;
