@@ -540,6 +540,44 @@ __device__ __forceinline__ void vx_gemv_i8b1(const vx_gemv_args& a) {
     }
 }
 
+// Batch 1: split float4 f of x (slot f & 15 of unit f >> 4) into the two
+// int8 levels of vx_i8lds and store them; the 8 float4 of a 32-block are 8
+// consecutive lanes, whose max and sums are reduced with DPP (every lane of
+// the wave takes part; `in` selects the lanes that store). The block stores
+// its scale c, sum(x) and -8 O, O = sum(254 x1 + x2) (|O| < 2^21: exact as a
+// float sum).
+__device__ __forceinline__ void vx_split_store_b1(const vx_i8lds& L, uint32_t f, f32x4 v, bool in) {
+    const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float c = m * (1.0f / (127.0f * 254.0f));
+    const float inv1 = m > 0.f ? 127.0f / m : 0.f;  // 1 / (254 c)
+    const float inv2 = inv1 * 254.0f;               // 1 / c
+    const float s1 = 254.0f * c;
+    int q1[4], q2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        q1[e] = (int)rintf(v[e] * inv1);
+        const float r = __builtin_fmaf(-(float)q1[e], s1, v[e]);
+        q2[e] = min(127, max(-127, (int)rintf(r * inv2)));
+    }
+    const float sx = vx_sum8((v.x + v.y) + (v.z + v.w));
+    // a non-finite block (fmaxf skips NaN; the sum does not) stores
+    // max + sum as its scale, so y is non-finite
+    const bool fin = m < __builtin_inff() && sx == sx;
+    const float oz = vx_sum8((float)(254 * (q1[0] + q1[1] + q1[2] + q1[3]) + (q2[0] + q2[1] + q2[2] + q2[3])));
+    if (in) {
+        const uint32_t ul = f >> 4, j = f & 15u;
+        uint32_t* x8 = (uint32_t*)L.x8(0);
+        x8[((0u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[0], q1[1], q1[2], q1[3]);
+        x8[((1u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
+        if ((j & 7u) == 0u) {
+            const uint32_t idx = 2u * ul + (j >> 3);
+            L.cs(1, 0)[idx] = fin ? c : m + sx;
+            L.sx(1, 0)[idx] = sx;
+            L.oz(1, 0)[idx] = -8 * (int)oz;
+        }
+    }
+}
+
 // Batch 1, persistent, on the integer-dot path: the work split, issue order
 // and ring of vx_gemv_p1, with x staged in LDS as two int8 levels per
 // 32-block (the vx_i8lds layout; x ~= c (254 x1 + x2), error <= c / 2 ~
@@ -604,44 +642,13 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         vx_load_unit<QT, true>(rp, u, wr[j]);
     }
 
-    // 3. split x into the two levels and store them with the block scale c,
-    //    sum(x) and -8 O, O = sum(254 x1 + x2) (|O| < 2^21: exact as a float
-    //    sum).
+    // 3. split x into the two levels and store them (vx_split_store_b1).
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
         if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
         const uint32_t f = t + XW * (uint32_t)i;
         const bool in = f < total;
-        const f32x4 v = in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f};
-        const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-        const float c = m * (1.0f / (127.0f * 254.0f));
-        const float inv1 = m > 0.f ? 127.0f / m : 0.f;  // 1 / (254 c)
-        const float inv2 = inv1 * 254.0f;               // 1 / c
-        const float s1 = 254.0f * c;
-        int q1[4], q2[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            q1[e] = (int)rintf(v[e] * inv1);
-            const float r = __builtin_fmaf(-(float)q1[e], s1, v[e]);
-            q2[e] = min(127, max(-127, (int)rintf(r * inv2)));
-        }
-        const float sx = vx_sum8((v.x + v.y) + (v.z + v.w));
-        // a non-finite block (fmaxf skips NaN; the sum does not) stores
-        // max + sum as its scale, so y is non-finite
-        const bool fin = m < __builtin_inff() && sx == sx;
-        const float oz = vx_sum8((float)(254 * (q1[0] + q1[1] + q1[2] + q1[3]) + (q2[0] + q2[1] + q2[2] + q2[3])));
-        if (in) {
-            const uint32_t ul = f >> 4, j = f & 15u;
-            uint32_t* x8 = (uint32_t*)L.x8(0);
-            x8[((0u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[0], q1[1], q1[2], q1[3]);
-            x8[((1u * 4u + (j >> 2)) * a.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[0], q2[1], q2[2], q2[3]);
-            if ((j & 7u) == 0u) {
-                const uint32_t idx = 2u * ul + (j >> 3);
-                L.cs(1, 0)[idx] = fin ? c : m + sx;
-                L.sx(1, 0)[idx] = sx;
-                L.oz(1, 0)[idx] = -8 * (int)oz;
-            }
-        }
+        vx_split_store_b1(L, f, in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f}, in);
     }
     __syncthreads();
 
