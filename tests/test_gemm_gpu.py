@@ -71,6 +71,25 @@ def test_tiled_parity(gemm, M, N, K):
     assert_close(c.cpu().numpy(), _f64(a, b)[0, 0], what=f"{M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,tr_b", [(67, 33, 17, False), (128, 256, 16, False), (129, 257, 31, True),
+                                        (300, 517, 129, False), (513, 1000, 100, True), (1024, 1024, 1024, False)])
+def test_wide_tiles_match_narrow(gemm, M, N, K, tr_b, monkeypatch):
+    """The 128 x 256 tile kernels (chosen for shapes such as 4096^3, forced
+    here with VX_GEMM_WIDE=1) give the same bits as the 128 x 128 ones: each
+    output is the same sum in the same order. Edge tiles in M, N and K."""
+    note(f"wide tiles {M}x{N}x{K} trB={tr_b}")
+    a = S.uniform((M, K), 5, DEV)
+    b = S.uniform((N, K), 6, DEV).t() if tr_b else S.uniform((K, N), 6, DEV)
+    c0, c1 = _nan(M, N), _nan(M, N)
+    monkeypatch.setenv("VX_GEMM_WIDE", "0")
+    gemm.dispatch(c0, a, b)
+    monkeypatch.setenv("VX_GEMM_WIDE", "1")
+    gemm.dispatch(c1, a, b)
+    torch.cuda.synchronize()
+    assert torch.equal(c0.view(torch.int32), c1.view(torch.int32))
+    assert_close(c1.cpu().numpy(), _f64(a, b.contiguous())[0, 0])
+
+
 @pytest.mark.parametrize("tr_a,tr_b", [(False, True), (True, False), (True, True)])
 def test_transposed_views(gemm, tr_a, tr_b):
     M, N, K = 200, 150, 130

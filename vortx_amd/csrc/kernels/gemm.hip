@@ -11,6 +11,9 @@
 //                  barrier per stage). Operand loads are 128-bit along the
 //                  contiguous dimension of each operand; edge tiles are
 //                  zero-filled like the reference (gemm.rs:102-106,121-125).
+//                  The _w kernels take 128x256 tiles (each wave 64x128, 2x4
+//                  accumulators, two workgroups per CU) with the same
+//                  per-output summation order, so the same bits.
 //  vx_gemv_f32     the N == 1 case: one wave per output row, 128-bit loads
 //                  along K, xor-shuffle reduction.
 #include <hip/hip_runtime.h>
@@ -68,19 +71,20 @@ extern "C" __global__ __launch_bounds__(64) void vx_gemm_naive(vx_gemm_args p) {
 // Global -> register fragment of one TBK slice of an operand tile.
 // "x" is the non-K dimension of the operand (M for A, N for B); sx/sk the
 // element strides along x and k; X the operand's extent along x.
-template <int MODE>
+template <int MODE, int TX>
 struct vx_frag {
-    float v[8];
+    float v[TX / 16];
 };
 
-template <int MODE>
-__device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base, int64_t sx, int64_t sk,
+template <int MODE, int TX>
+__device__ __forceinline__ void vx_load_frag(vx_frag<MODE, TX>& f, const float* base, int64_t sx, int64_t sk,
                                              uint32_t x0, uint32_t X, uint32_t k0, uint32_t K) {
     const uint32_t t = threadIdx.x;
+    constexpr uint32_t QX = TX / 4;  // float4 per k-row (MODE_XC)
     if constexpr (MODE == MODE_KC) {
-        // 128 x-rows of 4 float4 along k: element (x = f>>2, k = 4(f&3)).
+        // TX x-rows of 4 float4 along k: element (x = f>>2, k = 4(f&3)).
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
             const uint32_t x = x0 + (fi >> 2), k = k0 + 4u * (fi & 3u);
             const float* p = base + (int64_t)x * sx + k;
@@ -93,11 +97,11 @@ __device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base
             }
         }
     } else if constexpr (MODE == MODE_XC) {
-        // 16 k-rows of 32 float4 along x: element (k = f>>5, x = 4(f&31)).
+        // 16 k-rows of TX / 4 float4 along x: element (k = f / QX, x = 4(f % QX)).
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
-            const uint32_t k = k0 + (fi >> 5), x = x0 + 4u * (fi & 31u);
+            const uint32_t k = k0 + fi / QX, x = x0 + 4u * (fi % QX);
             const float* p = base + (int64_t)k * sk + x;
             if (k < K && x + 3 < X) {
                 const f32x4 q = *(const f32x4*)p;
@@ -108,11 +112,11 @@ __device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base
             }
         }
     } else {
-        // scalar: element (k = f>>7, x = f&127), f = t + 256 i.
+        // scalar: element (k = f / TX, x = f % TX), f = t + 256 i.
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < TX / 16; ++i) {
             const uint32_t fi = t + 256u * i;
-            const uint32_t k = k0 + (fi >> 7), x = x0 + (fi & 127u);
+            const uint32_t k = k0 + fi / TX, x = x0 + fi % TX;
             f.v[i] = (k < K && x < X) ? base[(int64_t)k * sk + (int64_t)x * sx] : 0.f;
         }
     }
@@ -121,40 +125,42 @@ __device__ __forceinline__ void vx_load_frag(vx_frag<MODE>& f, const float* base
 // The same fragment for a tile that lies inside the operand along x and a
 // stage that lies inside K: every load unconditional (no zero fill), so the
 // compiler counts outstanding loads exactly across the pipelined loop.
-template <int MODE>
-__device__ __forceinline__ void vx_load_frag_full(vx_frag<MODE>& f, const float* base, int64_t sx, int64_t sk,
+template <int MODE, int TX>
+__device__ __forceinline__ void vx_load_frag_full(vx_frag<MODE, TX>& f, const float* base, int64_t sx, int64_t sk,
                                                   uint32_t x0, uint32_t k0) {
     const uint32_t t = threadIdx.x;
+    constexpr uint32_t QX = TX / 4;
     if constexpr (MODE == MODE_KC) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
             const f32x4 q = *(const f32x4*)(base + (int64_t)(x0 + (fi >> 2)) * sx + k0 + 4u * (fi & 3u));
             f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
         }
     } else if constexpr (MODE == MODE_XC) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
-            const f32x4 q = *(const f32x4*)(base + (int64_t)(k0 + (fi >> 5)) * sk + x0 + 4u * (fi & 31u));
+            const f32x4 q = *(const f32x4*)(base + (int64_t)(k0 + fi / QX) * sk + x0 + 4u * (fi % QX));
             f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < TX / 16; ++i) {
             const uint32_t fi = t + 256u * i;
-            f.v[i] = base[(int64_t)(k0 + (fi >> 7)) * sk + (int64_t)(x0 + (fi & 127u)) * sx];
+            f.v[i] = base[(int64_t)(k0 + fi / TX) * sk + (int64_t)(x0 + fi % TX) * sx];
         }
     }
 }
 
 // Register fragment -> LDS tile S[k][x] (row pitch LD).
-template <int MODE, int LD>
-__device__ __forceinline__ void vx_store_frag(const vx_frag<MODE>& f, float* S) {
+template <int MODE, int TX, int LD>
+__device__ __forceinline__ void vx_store_frag(const vx_frag<MODE, TX>& f, float* S) {
     const uint32_t t = threadIdx.x;
+    constexpr uint32_t QX = TX / 4;
     if constexpr (MODE == MODE_KC) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
             const uint32_t x = fi >> 2, k = 4u * (fi & 3u);
 #pragma unroll
@@ -162,24 +168,25 @@ __device__ __forceinline__ void vx_store_frag(const vx_frag<MODE>& f, float* S) 
         }
     } else if constexpr (MODE == MODE_XC) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
-            const uint32_t k = fi >> 5, x = 4u * (fi & 31u);
+            const uint32_t k = fi / QX, x = 4u * (fi % QX);
             *(f32x4*)(S + k * LD + x) = f32x4{f.v[4 * i], f.v[4 * i + 1], f.v[4 * i + 2], f.v[4 * i + 3]};
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < TX / 16; ++i) {
             const uint32_t fi = t + 256u * i;
-            S[(fi >> 7) * LD + (fi & 127u)] = f.v[i];
+            S[(fi / TX) * LD + fi % TX] = f.v[i];
         }
     }
 }
 
-template <int AMODE, int BMODE>
+template <int AMODE, int BMODE, int TN>
 __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
+    constexpr int LDB = TN + LDS_PAD, NJ = TN / 64;  // per wave: 64 x TN / 2, NJ column blocks
     __shared__ float As[2][TBK * LDA_S];
-    __shared__ float Bs[2][TBK * LDB_S];
+    __shared__ float Bs[2][TBK * LDB];
 
     // Tile order: consecutive workgroup ids land on different XCDs (round
     // robin over 8), so ids are first regrouped per XCD, then walked in
@@ -193,7 +200,7 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     const uint32_t gsize = min(p.tiles_m - first_m, 8u);
     const uint32_t tm = first_m + (bid % group) % gsize;
     const uint32_t tn = (bid % group) / gsize;
-    const uint32_t m0 = tm * TBM, n0 = tn * TBN;
+    const uint32_t m0 = tm * TBM, n0 = tn * TN;
 
     const uint32_t z = blockIdx.z;
     const uint32_t bn = z / p.batch_c, bc = z % p.batch_c;
@@ -205,49 +212,52 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     const uint32_t wm = wave >> 1, wn = wave & 1u;
     const uint32_t l32 = lane & 31u, lk = lane >> 5;
 
-    f32x16 acc[2][2];
+    f32x16 acc[2][NJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
     // One TBK stage from LDS buffer `buf`.
     auto mma = [&](uint32_t buf) {
         const float* as = As[buf] + wm * 64u + l32;
-        const float* bs = Bs[buf] + wn * 64u + l32;
+        const float* bs = Bs[buf] + wn * (TN / 2u) + l32;
 #pragma unroll
         for (int ks = 0; ks < TBK / 2; ++ks) {
             const uint32_t kk = 2u * ks + lk;
             const float a0 = as[kk * LDA_S], a1 = as[kk * LDA_S + 32];
-            const float b0 = bs[kk * LDB_S], b1 = bs[kk * LDB_S + 32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            float b[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) b[j] = bs[kk * LDB + 32 * j];
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b[j], acc[0][j], 0, 0, 0);
+                acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b[j], acc[1][j], 0, 0, 0);
+            }
         }
     };
 
     const uint32_t nkf = p.K / TBK;  // whole stages
-    if (m0 + TBM <= p.M && n0 + TBN <= p.N) {
+    if (m0 + TBM <= p.M && n0 + TN <= p.N) {
         // Tile inside M and N: the loads for stage s + 2 are issued while
         // stage s is multiplied (two register buffers), so each load has two
         // stages of MFMAs to arrive before its LDS store waits for it. Stage
         // indices are clamped to the last whole stage (the extra loads at the
         // end are harmless). Unrolled by two so each buffer is named.
         if (nkf) {
-            vx_frag<AMODE> ra0, ra1;
-            vx_frag<BMODE> rb0, rb1;
-            auto ld = [&](uint32_t st, vx_frag<AMODE>& fa_, vx_frag<BMODE>& fb_) {
+            vx_frag<AMODE, TBM> ra0, ra1;
+            vx_frag<BMODE, TN> rb0, rb1;
+            auto ld = [&](uint32_t st, vx_frag<AMODE, TBM>& fa_, vx_frag<BMODE, TN>& fb_) {
                 const uint32_t k0 = min(st, nkf - 1u) * TBK;
-                vx_load_frag_full<AMODE>(fa_, A, p.as[2], p.as[3], m0, k0);
-                vx_load_frag_full<BMODE>(fb_, B, p.bs[3], p.bs[2], n0, k0);
+                vx_load_frag_full<AMODE, TBM>(fa_, A, p.as[2], p.as[3], m0, k0);
+                vx_load_frag_full<BMODE, TN>(fb_, B, p.bs[3], p.bs[2], n0, k0);
             };
             ld(0u, ra0, rb0);
             ld(1u, ra1, rb1);
-            vx_store_frag<AMODE, LDA_S>(ra0, As[0]);
-            vx_store_frag<BMODE, LDB_S>(rb0, Bs[0]);
+            vx_store_frag<AMODE, TBM, LDA_S>(ra0, As[0]);
+            vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
             __syncthreads();
             // Invariant at the top: stage st in buffer 0, stage st + 1 in
             // flight to ra1 / rb1.
@@ -258,14 +268,14 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
                 // below the other buffer's store and share its registers)
                 __builtin_amdgcn_sched_barrier(0);
                 mma(0u);
-                vx_store_frag<AMODE, LDA_S>(ra1, As[1]);
-                vx_store_frag<BMODE, LDB_S>(rb1, Bs[1]);
+                vx_store_frag<AMODE, TBM, LDA_S>(ra1, As[1]);
+                vx_store_frag<BMODE, TN, LDB>(rb1, Bs[1]);
                 __syncthreads();
                 ld(st + 3u, ra1, rb1);
                 __builtin_amdgcn_sched_barrier(0);
                 mma(1u);
-                vx_store_frag<AMODE, LDA_S>(ra0, As[0]);
-                vx_store_frag<BMODE, LDB_S>(rb0, Bs[0]);
+                vx_store_frag<AMODE, TBM, LDA_S>(ra0, As[0]);
+                vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
                 __syncthreads();
             }
             if (st < nkf) mma(0u);  // an odd stage count: the last one
@@ -273,38 +283,38 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
         if (p.K % TBK) {
             // the K tail: one stage zero-filled past K, through buffer 1
             // (its last reader finished before a barrier)
-            vx_frag<AMODE> fa;
-            vx_frag<BMODE> fb;
-            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, nkf * TBK, p.K);
-            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, nkf * TBK, p.K);
-            vx_store_frag<AMODE, LDA_S>(fa, As[1]);
-            vx_store_frag<BMODE, LDB_S>(fb, Bs[1]);
+            vx_frag<AMODE, TBM> fa;
+            vx_frag<BMODE, TN> fb;
+            vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, nkf * TBK, p.K);
+            vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, nkf * TBK, p.K);
+            vx_store_frag<AMODE, TBM, LDA_S>(fa, As[1]);
+            vx_store_frag<BMODE, TN, LDB>(fb, Bs[1]);
             __syncthreads();
             mma(1u);
         }
     } else {
         // Edge tile: zero-filled loads of the next stage during this one.
-        vx_frag<AMODE> fa;
-        vx_frag<BMODE> fb;
+        vx_frag<AMODE, TBM> fa;
+        vx_frag<BMODE, TN> fb;
         const uint32_t nk = (p.K + TBK - 1) / TBK;
         if (nk) {
-            vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
-            vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
-            vx_store_frag<AMODE, LDA_S>(fa, As[0]);
-            vx_store_frag<BMODE, LDB_S>(fb, Bs[0]);
+            vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
+            vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
+            vx_store_frag<AMODE, TBM, LDA_S>(fa, As[0]);
+            vx_store_frag<BMODE, TN, LDB>(fb, Bs[0]);
             __syncthreads();
         }
         for (uint32_t kt = 0; kt < nk; ++kt) {
             const uint32_t cur = kt & 1u;
             const bool more = kt + 1 < nk;
             if (more) {
-                vx_load_frag<AMODE>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
-                vx_load_frag<BMODE>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
+                vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
+                vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
             }
             mma(cur);
             if (more) {
-                vx_store_frag<AMODE, LDA_S>(fa, As[cur ^ 1u]);
-                vx_store_frag<BMODE, LDB_S>(fb, Bs[cur ^ 1u]);
+                vx_store_frag<AMODE, TBM, LDA_S>(fa, As[cur ^ 1u]);
+                vx_store_frag<BMODE, TN, LDB>(fb, Bs[cur ^ 1u]);
             }
             __syncthreads();
         }
@@ -315,8 +325,8 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = n0 + wn * 64u + 32u * j + l32;
+        for (int j = 0; j < NJ; ++j) {
+            const uint32_t col = n0 + wn * (TN / 2u) + 32u * j + l32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t row = m0 + wm * 64u + 32u * i + 8u * (v >> 2) + 4u * lk + (v & 3);
@@ -327,7 +337,7 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 }
 
 // WPE 3 (amdgpu_waves_per_eu(3, 4)) caps a kernel at 168 registers: three
-// 256-thread workgroups per CU. The two-stage prefetch's second register
+// 256-thread workgroups per CU (the wide kernels use ~245 under WPE 2: two). The two-stage prefetch's second register
 // buffer needs ~150-166 registers; squeezed into WPE 4's 128 (four
 // workgroups per CU) it ran slower: 4096^3 118.7 vs 123.5 TFLOP/s, B
 // transposed 126.4 vs 134.9, 1024^3 25.5 vs 29.8 (same-box A/B). The
@@ -335,7 +345,12 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 #define VX_GEMM_MFMA(AM, BM, NAME, WPE)                                                              \
     extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(WPE, 4)))    \
     void vx_gemm_mfma_##NAME(vx_gemm_args p) {                                                       \
-        vx_gemm_mfma<AM, BM>(p);                                                                     \
+        vx_gemm_mfma<AM, BM, 128>(p);                                                                \
+    }
+#define VX_GEMM_MFMA_W(AM, BM, NAME)                                                                 \
+    extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
+    void vx_gemm_mfma_##NAME##_w(vx_gemm_args p) {                                                   \
+        vx_gemm_mfma<AM, BM, 256>(p);                                                                \
     }
 // Suffix letters: A mode then B mode; k = contiguous along K,
 // x = contiguous along M / N, g = generic.
@@ -346,6 +361,8 @@ VX_GEMM_MFMA(MODE_XC, MODE_KC, xk, 3)
 VX_GEMM_MFMA(MODE_GEN, MODE_GEN, gg, 1)
 VX_GEMM_MFMA(MODE_KC, MODE_GEN, kg, 3)
 VX_GEMM_MFMA(MODE_GEN, MODE_XC, gx, 3)
+VX_GEMM_MFMA_W(MODE_KC, MODE_XC, kx)
+VX_GEMM_MFMA_W(MODE_KC, MODE_KC, kk)
 
 // ---------------------------------------------------------------- gemv
 // y[m] = sum_k A[m, k] x[k]; A contiguous along K with 16-byte aligned

@@ -351,7 +351,26 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
     const int am = operand_mode(p.l, 3, 2, p.nb, p.nc);
     const int bm = operand_mode(p.r, 2, 3, p.nb, p.nc);
     int k;
-    if (am == 0 && bm == 1) k = K_vx_gemm_mfma_kx;
+    // 128 x 256 tiles (two workgroups per CU) instead of 128 x 128 (three per
+    // CU) when they fill the last round of resident workgroups clearly
+    // better: 4096^3 is 1024 narrow tiles, 1.33 rounds of 768, but 512 wide
+    // ones, one round of 512. VX_GEMM_WIDE=0 / 1 forces the choice.
+    bool wide = false;
+    if (am == 0 && (bm == 0 || bm == 1)) {
+        const uint64_t tn = (uint64_t)a.tiles_m * a.tiles_n * batch;
+        const uint64_t tw = (uint64_t)a.tiles_m * ((p.N + 255) / 256) * batch;
+        const uint64_t sn = 3ull * (uint64_t)ctx->num_cus, sw = 2ull * (uint64_t)ctx->num_cus;
+        const double en = (double)tn / (double)(((tn + sn - 1) / sn) * sn);
+        const double ew = (double)tw / (double)(((tw + sw - 1) / sw) * sw);
+        wide = ew > en + 0.05;
+        const char* wenv = std::getenv("VX_GEMM_WIDE");
+        if (wenv && wenv[0] == '0') wide = false;
+        if (wenv && wenv[0] == '1') wide = true;
+    }
+    if (wide) {
+        a.tiles_n = (p.N + 255) / 256;
+        k = bm == 1 ? K_vx_gemm_mfma_kx_w : K_vx_gemm_mfma_kk_w;
+    } else if (am == 0 && bm == 1) k = K_vx_gemm_mfma_kx;
     else if (am == 0 && bm == 0) k = K_vx_gemm_mfma_kk;
     else if (am == 1 && bm == 1) k = K_vx_gemm_mfma_xx;
     else if (am == 1 && bm == 0) k = K_vx_gemm_mfma_xk;
