@@ -11,7 +11,9 @@ Secondary lines in the same JSON object: the other BASELINE GEMV configs
 Q4_0 4096 x 11008 b=1, Q4_0 11008 x 4096 b=4 and b=8, Q4_K 14336 x 4096
 b=16; GB/s of algorithmic bytes), the contiguous copy of a transposed
 8192^2 view and a plain streaming copy of a contiguous one (the achievable
-bandwidth beside the 8 TB/s peak), the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
+bandwidth beside the 8 TB/s peak), the same streaming copy at the headline's
+size (25.4 MB per launch, graph-replayed: the achievable rate of one launch
+that small), the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
 -> HBM upload (against the PCIe 5.0 x16 link) and the f32 GEMMs 4096^3,
 4096 x 11008 x 4096, 4096^3 with a transposed-B view and the broadcast
 batch (TFLOP/s), each with its roofline, plus CPU baselines from the
@@ -184,6 +186,53 @@ def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int)
     flops = 2.0 * B * M * N * K
     return {"value": flops * steps / wall / 1e12, "avg_launch_ms": e0.elapsed_time(e1) / steps, "flops": flops,
             "ms_per_step": wall * 1e3 / steps}
+
+
+def time_copy_like_gemv(nelem: int, steps: int, warmup: int):
+    """The achievable bandwidth of ONE launch as large as the headline GEMV:
+    Contiguous::launch of a contiguous f32 view of nelem elements (8 bytes
+    per element, read + write), sources rotating over >= 512 MB, K launches
+    captured into a HIP graph and replayed exactly as time_gemv does."""
+    import torch
+
+    import vortx_amd as vx
+
+    dev = torch.device("cuda:0")
+    shape = (nelem // 1024, 1024)
+    nsrc = -(-(512 << 20) // (4 * nelem)) + 1
+    srcs = [torch.randn(shape, device=dev) for _ in range(min(4, nsrc))]
+    log(f"[copies] {nsrc} x {4 * shape[0] * shape[1]}")
+    srcs = [srcs[i % len(srcs)].clone() for i in range(nsrc)]
+    out = torch.empty(shape, device=dev)
+    c = vx.Contiguous(0)
+    for i in range(warmup):
+        c.launch(out, srcs[i % nsrc])
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    chunk = min(steps, 500)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(chunk):
+                c.launch(out, srcs[i % nsrc], stream=s)
+    torch.cuda.synchronize()
+    reps = max(1, steps // chunk)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    done = reps * chunk
+    nbytes = 8 * out.numel()
+    return {"value": nbytes * done / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / done,
+            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / done, "sources": nsrc}
 
 
 def time_contiguous(shape, steps: int, warmup: int, transposed: bool = True):
@@ -402,6 +451,10 @@ def main() -> int:
     log(f"[contiguous] {cont}")
     copy = time_contiguous((8192, 8192), max(10, args.steps // 20), 5, transposed=False)
     log(f"[copy] {copy}")
+    # one launch moving the headline GEMV's bytes (25,422,848 / 8 elements,
+    # rounded up to whole rows of 1024): what a single launch of that size reaches
+    copy25 = time_copy_like_gemv(3104 * 1024, args.steps, args.warmup)
+    log(f"[copy_25mb] {copy25}")
     quant = []
     for qt, label in ((8, "q8_0"), (12, "q4_k")):
         r = time_quantize(qt, 14336, 4096, max(10, args.steps // (20 if qt == 8 else 100)), 3)
@@ -455,6 +508,11 @@ def main() -> int:
                          "bandwidth of a plain read + write stream on this GPU)",
              "value": copy["value"], "unit": "GB/s", "ms_per_step": copy["ms_per_step"],
              "roofline": roof_hbm(copy, "copy_8192")},
+            {"workload": "streaming copy of the headline's size: Contiguous::launch of a contiguous 3104x1024 f32 "
+                         "view, 25.43 MB read + written per launch (the headline GEMV moves 25.42 MB), sources "
+                         "rotating over >= 512 MB, HIP-graph replay (the achievable rate of one launch this size)",
+             "value": copy25["value"], "unit": "GB/s", "ms_per_step": copy25["ms_per_step"],
+             "roofline": roof_hbm(copy25, "copy_3104x1024")},
         ] + [
             {"workload": f"quantize f32 14336x4096 to {label.upper()} blocks (ggml reference quantizer)",
              "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
