@@ -1019,6 +1019,9 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
     float acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = 0.f;
+    i32x4 areg[NCP][2];
+#pragma unroll
+    for (int cp = 0; cp < NCP; ++cp) areg[cp][0] = areg[cp][1] = i32x4{0, 0, 0, 0};
     uint32_t ts = 0, k = 0;
     auto body = [&](uint32_t (&rl)[NW]) {
         const uint32_t q = wave + 16u * k;  // round of this tile
@@ -1039,17 +1042,25 @@ __device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
             // T = 254 D_L0 + D_L1 (|D| < 2^20: exact in int32).
             const i32x4 z = i32x4{0, 0, 0, 0};
             float tq[NCP][2][2];
+            // Only the 16 lanes inside their k-group's A rows load (columns >=
+            // B read the 64 zero bytes at a.upitch); the other lanes' A
+            // registers were zeroed once and are never written.
 #pragma unroll
             for (int bb = 0; bb < 2; ++bb) {
+                if (a_on) {
+#pragma unroll
+                    for (int cp = 0; cp < NCP; ++cp) {
+                        const uint8_t* ap = xq + abase[cp] + 32u * bb;
+                        areg[cp][0] = *(const i32x4*)ap;
+                        areg[cp][1] = *(const i32x4*)(ap + 16u);
+                    }
+                }
                 const i32x4 bw0 = bb ? vx_m_piece<QT, 2>(r) : vx_m_piece<QT, 0>(r);
                 const i32x4 bw1 = bb ? vx_m_piece<QT, 3>(r) : vx_m_piece<QT, 1>(r);
 #pragma unroll
                 for (int cp = 0; cp < NCP; ++cp) {
-                    // lanes outside their k-group's A rows (and columns >= B)
-                    // read the 64 zero bytes at a.upitch
-                    const uint8_t* ap = xq + abase[cp] + 32u * bb;
-                    const i32x4 a0 = *(const i32x4*)ap;
-                    const i32x4 a1 = *(const i32x4*)(ap + 16u);
+                    const i32x4 a0 = areg[cp][0];
+                    const i32x4 a1 = areg[cp][1];
                     i32x4 dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bw0, z, 0, 0, 0);
                     dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bw1, dd, 0, 0, 0);
                     tq[cp][0][bb] = (float)(__mul24(dd[0], 254) + dd[1]);
