@@ -81,13 +81,29 @@ def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False
 @pytest.mark.parametrize("B", [1, 2, 3, 4, 8, 16, 21])
 # (93, 832): 13 units of 64, so the batched kernel's last round is ragged
 # (Q4_K skips: K is not a multiple of 256); (1, 4096): a single row.
-@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536), (93, 832), (1, 4096)])
+# (61, 8128) and (57, 16384): two passes of 64 units (the last one partial)
+# and four, the batch-1 kernel's K limit.
+@pytest.mark.parametrize("M,K", [(131, 4096), (70, 11008), (257, 1536), (93, 832), (1, 4096), (61, 8128),
+                                 (57, 16384)])
 def test_gemv_parity_small(qgemv, qtype, B, M, K):
     if K % O.QTYPE_INFO[qtype][0]:
         pytest.skip("K not a multiple of the block size")
     note(f"gemv {QN[qtype]} M={M} K={K} B={B}")
     got, ref = _run_gemv(qgemv, qtype, M, K, B, seed=M + K + B)
     assert_close(got, ref, what=f"{QN[qtype]} {M}x{K} b{B}")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("M,K", [(9000, 8192), (5000, 16384), (4097, 11008)])
+def test_gemv_b1_multipass_several_rows(qgemv, qtype, M, K):
+    """Batch 1 with K > 4096 (several passes of 64 units per row) and more
+    rows than the grid has waves, so a wave's items run across rows and
+    passes through both ring slots."""
+    if K % O.QTYPE_INFO[qtype][0]:
+        pytest.skip("K not a multiple of the block size")
+    note(f"gemv b1 multipass {QN[qtype]} M={M} K={K}")
+    got, ref = _run_gemv(qgemv, qtype, M, K, 1, seed=M + K)
+    assert_close(got, ref, what=f"{QN[qtype]} {M}x{K} b1")
 
 
 # BASELINE.json configs at full size.
