@@ -579,7 +579,14 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
             lds = (size_t)a.upitch * 152u;
-            s = launch(ctx, p1i_kernel(w->qtype, 2), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
+            // Ring of two items per wave; Q8_0 (68-byte units) with at most two
+            // items per wave takes a ring of one: the second slot would only
+            // load a repeat of the last item (2048 x 4096 4.57 -> 4.09 us,
+            // 4096 x 8192 8.75 -> 8.45 us, 4096 x 4096 5.45 -> 5.42 us).
+            const uint32_t waves = (uint32_t)ctx->num_cus * 16u;
+            const uint32_t items = (M + waves - 1u) / waves * ((a.nunits + 63u) / 64u);
+            const int ring = (w->qtype == VX_Q8_0 && items <= 2u) ? 1 : 2;
+            s = launch(ctx, p1i_kernel(w->qtype, ring), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
