@@ -44,6 +44,12 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, public spec
 F32_MFMA_PEAK_TFS = 157.3   # MI355X dense f32 matrix, public spec
 PCIE_PEAK_GBS = 64.0        # host link: PCIe 5.0 x16, one direction
 METRIC = "Q4_0/Q8_0 GEMV HBM GB/s at 11008x4096 b=1; f32 GEMM TFLOP/s at 4096^3"
+# What the default GEMV path computes in: x split per 32-element block into two
+# int8 levels with one f32 scale, products and block sums with the exactly
+# decoded weights in int32, scaling and accumulation in f32.
+DT_INT8X = "int8 x int4/int8 -> int32, f32 scale and accumulate"
+X_REPR = ("x rounded per 32-element block to c (254 x1 + x2), x1 and x2 int8, c ~ max|x_blk| / 32000: "
+          "|error| <= c / 2 ~ 1.6e-5 max|x_blk| per element")
 
 
 def log(msg: str) -> None:
@@ -64,7 +70,7 @@ def load_traffic(name: str):
     return None
 
 
-def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str):
+def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str, x_f32: bool = False):
     import torch
 
     import vortx_amd as vx
@@ -85,7 +91,7 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     xv, yv = x.t(), y.t()
 
     for i in range(warmup):
-        g.dispatch(yv, qws[i % ncopy], xv)
+        g.dispatch(yv, qws[i % ncopy], xv, x_f32=x_f32)
     torch.cuda.synchronize()
 
     # K launches captured once into a HIP graph (chunks of <= 500 nodes) on
@@ -99,7 +105,7 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     with torch.cuda.stream(s):
         with torch.cuda.graph(graph, stream=s):
             for i in range(chunk):
-                g.dispatch(yv, qws[i % ncopy], xv, stream=s)
+                g.dispatch(yv, qws[i % ncopy], xv, stream=s, x_f32=x_f32)
     torch.cuda.synchronize()
     reps = max(1, steps // chunk)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -421,6 +427,10 @@ def main() -> int:
 
     q40 = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0")
     log(f"[q4_0] {q40}")
+    # The same headline config with x kept in f32 (VX_GEMV_X_F32): f32 FMA on
+    # the exactly decoded weights, the exact-arithmetic twin of the default.
+    q40f = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0_f32x", x_f32=True)
+    log(f"[q4_0_f32x] {q40f}")
     # secondary GEMV configs: (qtype, M, K, B, label, workload, traffic profile)
     SECONDARY = [
         (8, 4096, 4096, 1, "q8_0", "Q8_0 GEMV 4096x4096 batch 1", "gemv_q8_0_4096x4096_b1"),
@@ -429,8 +439,11 @@ def main() -> int:
         (12, 14336, 4096, 1, "q4_k_14336", "Q4_K GEMV 14336x4096 batch 1", "gemv_q4_k_14336x4096_b1"),
         (2, 11008, 4096, 4, "q4_0_b4", "Q4_0 GEMV 11008x4096 batch 4", "gemv_q4_0_11008x4096_b4"),
         (2, 11008, 4096, 8, "q4_0_b8", "Q4_0 GEMV 11008x4096 batch 8", "gemv_q4_0_11008x4096_b8"),
+        (2, 4096, 11008, 4, "q4_0_t_b4", "Q4_0 GEMV 4096x11008 batch 4", "gemv_q4_0_4096x11008_b4"),
+        (2, 4096, 11008, 8, "q4_0_t_b8", "Q4_0 GEMV 4096x11008 batch 8", "gemv_q4_0_4096x11008_b8"),
         (8, 4096, 4096, 8, "q8_0_b8", "Q8_0 GEMV 4096x4096 batch 8", "gemv_q8_0_4096x4096_b8"),
         (12, 14336, 4096, 16, "q4_k_b16", "Q4_K GEMV 14336x4096 batch 16", "gemv_q4_k_14336x4096_b16"),
+        (12, 32000, 4096, 16, "q4_k_32000_b16", "Q4_K GEMV 32000x4096 batch 16", "gemv_q4_k_32000x4096_b16"),
     ]
     sec = []
     for qt, M, K, B, label, workload, prof in SECONDARY:
@@ -490,16 +503,21 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": DT_INT8X,
         "data": "synthetic",
         "config": {"workload": "Q4_0 GEMV y=Wx, W 11008x4096 (GGML Q4_0 blocks), batch 1",
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
-                   "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches"},
+                   "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches",
+                   "x_repr": X_REPR},
         "roofline": roof_hbm(q40, "gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
         "secondary": [
+            {"workload": "Q4_0 GEMV 11008x4096 batch 1, x kept in f32 (VX_GEMV_X_F32: f32 FMA on the exactly "
+                         "decoded weights)", "value": q40f["value"], "unit": "GB/s", "ms_per_step": q40f["ms_per_step"],
+             "dtype": "f32", "roofline": roof_hbm(q40f, "gemv_q4_0_11008x4096_b1_f32x")},
+        ] + [
             {"workload": wl, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
-             "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
+             "dtype": DT_INT8X, "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
         ] + [
             {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
              "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],

@@ -188,10 +188,14 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
 /* ------------------------------------------------------------------ */
 
 /* y[m, b] = sum_k W[m, k] * x[k, b] with W decoded exactly from its
- * blocks and f32 accumulation. y is an [M, B] view, x a [K, B] view
- * (rank 1 views mean B = 1); any strides. Fast path: x with stride 1
- * along K (activations stored [B, K]). Same operand roles as
- * Gemm::dispatch(out = y, lhs = W, rhs = x). */
+ * blocks. y is an [M, B] view, x a [K, B] view (rank 1 views mean B = 1);
+ * any strides. Fast path: x with stride 1 along K (activations stored
+ * [B, K]). Same operand roles as Gemm::dispatch(out = y, lhs = W, rhs = x).
+ * Arithmetic: this is vx_gemv_q_ex with flags 0, so x is NOT kept in f32:
+ * each 32-element block of each column is rounded to two int8 levels with
+ * one f32 scale (|error| <= ~1.6e-5 of the block's max|x|), the products
+ * with the weights are exact int32 and the scaling and accumulation are
+ * f32. vx_gemv_q_ex(..., VX_GEMV_X_F32) keeps x in f32. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 

@@ -381,6 +381,32 @@ int orc_contiguous_u32(uint32_t* dest, const uint32_t* src, const uint32_t* size
 }
 
 /* ------------------------------------------------------------- quantize */
+/*
+ * ggml MIT license notice (the quantizers below restate ggml's published
+ * quantize_row_*_ref / make_qkx2_quants; ggml is distributed under it):
+ *
+ *   MIT License
+ *
+ *   Copyright (c) 2023-2024 The ggml authors
+ *
+ *   Permission is hereby granted, free of charge, to any person obtaining a copy
+ *   of this software and associated documentation files (the "Software"), to deal
+ *   in the Software without restriction, including without limitation the rights
+ *   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+ *   copies of the Software, and to permit persons to whom the Software is
+ *   furnished to do so, subject to the following conditions:
+ *
+ *   The above copyright notice and this permission notice shall be included in all
+ *   copies or substantial portions of the Software.
+ *
+ *   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+ *   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+ *   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+ *   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+ *   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+ *   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+ *   SOFTWARE.
+ */
 /* IEEE binary32 -> binary16, round to nearest even (what ggml's
  * GGML_FP32_TO_FP16 does with F16C or its software path). */
 uint16_t orc_f32_to_f16(float f) {

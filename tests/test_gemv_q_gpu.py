@@ -110,7 +110,7 @@ def test_gemv_b1_multipass_several_rows(qgemv, qtype, M, K):
 FULL = [
     (vx.VX_Q8_0, 4096, 4096, 1), (vx.VX_Q8_0, 4096, 4096, 8),
     (vx.VX_Q4_0, 11008, 4096, 1), (vx.VX_Q4_0, 11008, 4096, 4), (vx.VX_Q4_0, 11008, 4096, 8),
-    (vx.VX_Q4_0, 4096, 11008, 1),
+    (vx.VX_Q4_0, 4096, 11008, 1), (vx.VX_Q4_0, 4096, 11008, 4), (vx.VX_Q4_0, 4096, 11008, 8),
     (vx.VX_Q4_K, 14336, 4096, 1), (vx.VX_Q4_K, 14336, 4096, 16),
     (vx.VX_Q4_K, 32000, 4096, 1), (vx.VX_Q4_K, 32000, 4096, 16),
 ]

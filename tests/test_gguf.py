@@ -207,6 +207,9 @@ def _bad_files():
     yield "negative ne", raw("w", [32, 2 ** 63], 8, 0, q8)
     yield "element count overflow", raw("w", [2 ** 40, 2 ** 40], 0, 0)
     yield "byte size overflow", raw("w", [2 ** 32, 2 ** 31 - 1], 0, 0)
+    # one row of 2^62 + 1 f32 elements: 4 (2^62 + 1) wraps to 4 bytes in u64
+    yield "row byte size overflow (f32)", raw("w", [2 ** 62 + 1], 0, 0, bytes(32))
+    yield "row byte size overflow (i64)", raw("w", [2 ** 61 + 1, 1], 27, 0, bytes(32))
     yield "misaligned offset", raw("w", [32, 1], 8, 16, bytes(64))
     yield "data past the end", raw("w", [32, 1], 8, 0, bytes(33))
     yield "offset past the end", raw("w", [32, 1], 8, 1 << 40, q8)

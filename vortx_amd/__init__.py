@@ -28,7 +28,7 @@ from . import _ffi
 from ._ffi import (NONE_STRIDE, ROUTE_EMPTY, ROUTE_GEMV, ROUTE_NAIVE, ROUTE_TILED, VX_Q4_0, VX_Q4_K, VX_Q8_0,
                    VortxError, check, lib)
 
-__all__ = ["TensorLayout", "Gemm", "QuantGemv", "QWeight", "Contiguous", "GGUFFile", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
+__all__ = ["TensorLayout", "layout_extent", "Gemm", "QuantGemv", "QWeight", "Contiguous", "GGUFFile", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
            "ROUTE_NAIVE", "ROUTE_TILED", "ROUTE_GEMV", "ROUTE_EMPTY", "qtype_info", "lib"]
 
 # Load eagerly: a missing library must fail at import, not at first call.
@@ -107,6 +107,16 @@ class TensorLayout:
         return bool(lib().vx_layout_is_contiguous(C.byref(self._c())))
 
 
+def layout_extent(layout: TensorLayout) -> int:
+    """Elements a buffer needs to hold every element of ``layout``: its offset
+    plus the largest index sum((size - 1) * stride) plus one (0 when a
+    dimension below rank is empty)."""
+    dims = layout.size[:layout.rank]
+    if any(d == 0 for d in dims):
+        return 0
+    return layout.offset + sum((d - 1) * st for d, st in zip(dims, layout.stride[:layout.rank])) + 1
+
+
 def _view_of(v, mutable: bool, any4: bool = False):
     """torch tensor or (buffer, TensorLayout) -> VxCView / VxMView.
     any4: accept any 4-byte element type (bit copies), not only float32."""
@@ -114,7 +124,15 @@ def _view_of(v, mutable: bool, any4: bool = False):
     ok = (lambda t: t.element_size() == 4) if any4 else (lambda t: t.dtype == torch.float32)
     if isinstance(v, tuple):
         buf, layout = v
-        if not (isinstance(buf, torch.Tensor) and ok(buf) and buf.is_cuda):
+        if not (isinstance(buf, torch.Tensor) and ok(buf)):
+            raise TypeError("view buffer must be a float32 tensor on the GPU")
+        # The C ABI carries no buffer sizes: a layout reaching past the buffer
+        # would become an out-of-bounds device access, so it is refused here.
+        need = layout_extent(layout)
+        if need > buf.numel():
+            raise VortxError(_ffi.VX_ERR_INVALID,
+                             f"layout {layout} reaches element {need - 1} of a {buf.numel()}-element buffer")
+        if not buf.is_cuda:
             raise TypeError("view buffer must be a float32 tensor on the GPU")
         base = buf.data_ptr()
     else:
@@ -221,6 +239,15 @@ class QWeight:
         qk, bb = qtype_info(self.qtype)
         if self.row_stride == 0:
             self.row_stride = self.cols // qk * bb
+        # The C ABI carries no buffer size: an undersized buffer would be read
+        # out of bounds on the device, so it is refused here.
+        if self.rows and self.cols:
+            need = (self.rows - 1) * self.row_stride + self.cols // qk * bb
+            have = self.data.numel() * self.data.element_size()
+            if have < need:
+                raise VortxError(_ffi.VX_ERR_INVALID,
+                                 f"QWeight needs {need} bytes ({self.rows} rows at stride {self.row_stride}), "
+                                 f"the buffer holds {have}")
 
     def _c(self) -> _ffi.VxQWeight:
         w = _ffi.VxQWeight()

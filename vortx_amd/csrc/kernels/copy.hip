@@ -39,8 +39,11 @@ __device__ __forceinline__ uint32_t vx_div(uint32_t n, const vx_udiv& d) {
 
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_gen(vx_copy_args a) {
     const int64_t off = a.dev_offset ? (int64_t)*a.dev_offset : 0;
-    const uint32_t stride = gridDim.x * 256u;
-    for (uint32_t i = blockIdx.x * 256u + threadIdx.x; i < a.total; i += stride) {
+    // 64-bit loop index: with total just below 2^32, a u32 i + stride would
+    // wrap below total and the loop would never end
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t i64 = (uint64_t)blockIdx.x * 256u + threadIdx.x; i64 < a.total; i64 += stride) {
+        const uint32_t i = (uint32_t)i64;          // < total < 2^32
         const uint32_t r1 = vx_div(i, a.dw);       // i / W
         const uint32_t w = i - r1 * a.size[3];
         const uint32_t r2 = vx_div(r1, a.dh);      // / H
@@ -59,9 +62,9 @@ extern "C" __global__ __launch_bounds__(256) void vx_contiguous_gen(vx_copy_args
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_v4(vx_copy_args a) {
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const uint32_t total4 = a.total >> 2;
-    const uint32_t stride = gridDim.x * 256u;
-    for (uint32_t i4 = blockIdx.x * 256u + threadIdx.x; i4 < total4; i4 += stride) {
-        const uint32_t i = i4 << 2;
+    const uint64_t stride = (uint64_t)gridDim.x * 256u;
+    for (uint64_t j = (uint64_t)blockIdx.x * 256u + threadIdx.x; j < total4; j += stride) {
+        const uint32_t i = (uint32_t)j << 2;
         const uint32_t r1 = vx_div(i, a.dw);
         const uint32_t w = i - r1 * a.size[3];
         const uint32_t r2 = vx_div(r1, a.dh);

@@ -16,6 +16,31 @@
 //                             super-block maxima, the 6-bit scale packing
 //                             and the nibble pairs (compute-bound: about
 //                             20 search passes of 32 elements per lane).
+//
+// ggml MIT license notice (the quantizers below restate ggml's published
+// quantize_row_*_ref / make_qkx2_quants; ggml is distributed under it):
+//
+//   MIT License
+//
+//   Copyright (c) 2023-2024 The ggml authors
+//
+//   Permission is hereby granted, free of charge, to any person obtaining a copy
+//   of this software and associated documentation files (the "Software"), to deal
+//   in the Software without restriction, including without limitation the rights
+//   to use, copy, modify, merge, publish, distribute, sublicense, and/or sell
+//   copies of the Software, and to permit persons to whom the Software is
+//   furnished to do so, subject to the following conditions:
+//
+//   The above copyright notice and this permission notice shall be included in all
+//   copies or substantial portions of the Software.
+//
+//   THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR
+//   IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF MERCHANTABILITY,
+//   FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT SHALL THE
+//   AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER
+//   LIABILITY, WHETHER IN AN ACTION OF CONTRACT, TORT OR OTHERWISE, ARISING FROM,
+//   OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER DEALINGS IN THE
+//   SOFTWARE.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -165,7 +190,8 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q8_0(vx_quant_args
 extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_0(vx_quant_args a) {
     const uint32_t b = blockIdx.x * 256u + threadIdx.x;
     if (b >= a.nblk) return;
-    for (uint32_t row = blockIdx.y; row < a.M; row += gridDim.y) {
+    for (uint64_t r64 = blockIdx.y; r64 < a.M; r64 += gridDim.y) {  // 64-bit: no wrap near 2^32 rows
+        const uint32_t row = (uint32_t)r64;
         float x[32];
         vx_q_load32(a, row, 32u * b, x);
         uint16_t w[9];

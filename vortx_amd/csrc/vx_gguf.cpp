@@ -268,7 +268,10 @@ int parse(vx_gguf_file* f) {
         uint32_t be, bb;
         if (type_size(t.type, &be, &bb)) {
             if (t.ne[0] % be) return bad("tensor '" + t.name + "' ne[0] is not a multiple of its block size");
-            uint64_t n = t.ne[0] / be * bb;  // bytes per row, <= 2^63 / 32 * 292
+            // bytes per row; for one-element "blocks" (F32, I64, ...) bb alone can
+            // carry ne[0] < 2^63 past 2^64
+            if (t.ne[0] / be > UINT64_MAX / bb) return bad("tensor '" + t.name + "' byte size overflows");
+            uint64_t n = t.ne[0] / be * bb;
             for (uint32_t d = 1; d < t.n_dims; ++d) {
                 if (t.ne[d] && n > UINT64_MAX / t.ne[d]) return bad("tensor '" + t.name + "' byte size overflows");
                 n *= t.ne[d];
