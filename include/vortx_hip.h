@@ -15,7 +15,10 @@
  *  - Launches are asynchronous on the given stream (NULL = null stream).
  *    The caller keeps every buffer alive until the stream work completes;
  *    the library never frees or retains caller memory.
- *  - A vx_ctx is immutable after vx_init and may be shared by threads.
+ *  - A vx_ctx may be shared by threads. Its one piece of mutable state is
+ *    the activation workspace of vx_gemv_q / vx_gemv_q_ex at B >= 2 (see
+ *    there): such calls on one context must not overlap in time on
+ *    different streams.
  */
 #ifndef VORTX_HIP_H
 #define VORTX_HIP_H
@@ -152,7 +155,13 @@ typedef enum vx_gemm_flags {
      * that operand is then reused along the dim (stride 0), the semantics
      * of TensorLayout::broadcast (src/shapes.rs:346-391) that the reference
      * leaves as a TODO in Gemm::dispatch (src/linalg/gemm.rs:64). */
-    VX_GEMM_BROADCAST = 1
+    VX_GEMM_BROADCAST = 1,
+    /* Tile shape of the MFMA kernel, for callers that pin it (both give the
+     * same bits; by default the one that fills the GPU's last round of
+     * resident workgroups better is taken): 128 x 128 or 128 x 256 output
+     * tiles. Exclusive; ignored on the naive and GEMV routes. */
+    VX_GEMM_TILE_NARROW = 2,
+    VX_GEMM_TILE_WIDE = 4
 } vx_gemm_flags;
 
 typedef struct vx_gemm_opts {
@@ -195,7 +204,14 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
  * each 32-element block of each column is rounded to two int8 levels with
  * one f32 scale (|error| <= ~1.6e-5 of the block's max|x|), the products
  * with the weights are exact int32 and the scaling and accumulation are
- * f32. vx_gemv_q_ex(..., VX_GEMV_X_F32) keeps x in f32. */
+ * f32. vx_gemv_q_ex(..., VX_GEMV_X_F32) keeps x in f32.
+ * With B >= 2 (fast layouts) x is split by vx_quantize_x into a workspace
+ * the context owns (allocated on first use and grown when a call needs more;
+ * growing synchronizes the device), then vx_gemv_q_xq runs: calls of
+ * one context must therefore not overlap in time on different streams, and
+ * the first call of a given size must not be made during stream capture
+ * (VX_ERR_UNSUPPORTED then). Callers that cannot allocate use
+ * vx_quantize_x + vx_gemv_q_xq on buffers of their own. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 
@@ -206,12 +222,58 @@ int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
  * weights are exact in int32 and the scaling is f32. Batch 1 reduces with
  * v_dot4_i32_i8, batches (B >= 2) on the int8 matrix cores. VX_GEMV_X_F32
  * keeps x in f32 instead (f32 FMA on the exactly decoded weights; slower);
- * VX_GEMV_X_INT8 names the default split and may not be combined with it.
- * The environment variable VX_GEMV_BATCHED=simt selects the exact-f32
- * kernels for batches only. */
+ * VX_GEMV_X_INT8 names the default split and may not be combined with it. */
 typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1, VX_GEMV_X_F32 = 2 } vx_gemv_flags;
 int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_cview* x, uint32_t flags);
+
+/* ---- activation split: x -> two int8 levels per 32-block (VX_XQ) -----
+ * No counterpart in the reference (it has no quantized code): the step
+ * before the batched GEMV, done once per x so that every CU of the GEMV
+ * reads 2.25 bytes per element instead of re-splitting 4.
+ * Column b of x [K, B], 32-element block j, values v[0..31]:
+ *   m = max|v|, S = sum v (pairs within each 4, then the 8 partial sums
+ *   pairwise), c1 = m / 126, c2 = c1 / 254, i1 = 126 / m (0 when m < 2^-100
+ *   or the block holds a NaN / inf), i2 = 254 i1,
+ *   q1 = clamp(rne(v i1), +-127), q2 = clamp(rne(fma(-q1, c1, v) i2), +-127)
+ * (every operation one IEEE f32 rounding), so x ~= c2 (254 q1 + q2) with
+ * |error| <= ~max|v| / 64008 per element. Element i of a block sits at
+ * position p(i) = 8 (i/4) + i%4 (i < 16) or 8 ((i-16)/4) + 4 + i%4 (i >= 16),
+ * the order of a Q4_0 block's nibbles. Layout in one device buffer, with
+ * NI = ceil(K / 256) items of 8 blocks:
+ *   levels int8 at byte 0: level L of column b, block j, position p at
+ *     ((j/8 B + b) 2 + L) 256 + (p/8) 64 + (j%8) 8 + p%8 (the 8 bytes one
+ *     matrix-core lane takes from each of an item's 8 blocks lie together;
+ *     blocks past K/32 in the last item are unused);
+ *   scales f32 [K/32][B][2] at byte NI B 512: {c2, S}, or {m + S, S}
+ *     (non-finite) for a block holding a NaN or inf.
+ * The bytes are deterministic and equal a sequential CPU evaluation of the
+ * formulas (the tests check them byte for byte). */
+typedef struct vx_xq {
+    void* base;   /* device buffer, 16-byte aligned, >= vx_xq_size(K, B) bytes */
+    uint32_t K;   /* elements per column, a multiple of 32 */
+    uint32_t B;   /* columns */
+} vx_xq;
+
+/* Bytes of the vx_xq of a [K, B] x: ceil(K/256) * B * 512 + (K/32) * B * 8
+ * (72 bytes per 32 elements when K is a multiple of 256). VX_ERR_UNSUPPORTED
+ * when K is not a multiple of 32. */
+int vx_xq_size(uint32_t K, uint32_t B, uint64_t* bytes);
+
+/* Write the split of x (a [K, B] f32 view, any strides; rank 1 means B = 1)
+ * into out. Asynchronous on `stream`. */
+int vx_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* out, const vx_cview* x);
+
+/* y = W x with x given by its split (written by vx_quantize_x; out->K ==
+ * w->cols): the batched GEMV without the split, for callers that reuse one
+ * x for several matrices (a layer's q / k / v or gate / up projections) and
+ * quantize it once. y is an [M, B] view, any strides. Needs K a multiple
+ * of 64 and W rows 4-byte aligned, else VX_ERR_UNSUPPORTED. Products of the
+ * levels with the exactly decoded weights are exact int32 on the int8
+ * matrix cores; scaling and accumulation are f32. The library allocates
+ * nothing here. */
+int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y,
+                 const vx_qweight* w, const vx_xq* x);
 
 /* out[m, k] = W[m, k] decoded to f32 (bit-exact: every block value is
  * exactly representable in f32). out is an [M, K] view, any strides. */

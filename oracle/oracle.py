@@ -63,6 +63,9 @@ def lib():
         L.orc_f32_to_f16.restype = C.c_uint16
         L.orc_quantize.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_uint64]
         L.orc_quantize.restype = C.c_int
+        L.orc_quantize_x.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p,
+                                     C.c_void_p]
+        L.orc_quantize_x.restype = C.c_int
         for name in ("orc_dequant", "orc_gemv_q_f64", "orc_gemv_q_f32_omp", "orc_gemm_ref_f32",
                      "orc_gemm_f64", "orc_gemm_tiled_f32_omp", "orc_q4k_scale_min"):
             if name != "orc_q4k_scale_min":
@@ -234,3 +237,44 @@ def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
     rc = lib().orc_quantize(qtype, _ptr(x), M, K, K, _ptr(out), rb)
     assert rc == 0, rc
     return out
+
+
+# ---------------------------------------------------- activation split
+# Byte position of element i of a 32-block in the level arrays (the order of
+# a Q4_0 block's nibbles: byte t holds elements t and t + 16).
+XQ_POS = np.array([8 * (i // 4) + i % 4 if i < 16 else 8 * ((i - 16) // 4) + 4 + (i - 16) % 4 for i in range(32)])
+
+
+def quantize_x(x_bk: np.ndarray):
+    """x f32 [B, K] (column b of the GEMV's [K, B] operand in row b) ->
+    (levels int8 [K/32, B, 2, 32], scales f32 [K/32, B, 2]) as restated in
+    vx_oracle.c orc_quantize_x (levels in XQ_POS order)."""
+    x = np.ascontiguousarray(x_bk, dtype=np.float32)
+    B, K = x.shape
+    assert K % 32 == 0
+    levels = np.zeros((K // 32, B, 2, 32), dtype=np.int8)
+    scales = np.zeros((K // 32, B, 2), dtype=np.float32)
+    rc = lib().orc_quantize_x(_ptr(x), 1, K, K, B, _ptr(levels), _ptr(scales))
+    assert rc == 0, rc
+    return levels, scales
+
+
+def xq_decode_f64(levels: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """The x an activation split stands for, in float64: [B, K] with
+    x[b, 32 j + i] = c2 (254 q1 + q2) at position XQ_POS[i] of block j."""
+    nblk, B = levels.shape[:2]
+    lv = levels.astype(np.float64)[:, :, :, XQ_POS]          # [nblk, B, 2, 32] in element order
+    val = scales[:, :, 0:1].astype(np.float64) * (254.0 * lv[:, :, 0] + lv[:, :, 1])
+    return val.transpose(1, 0, 2).reshape(B, nblk * 32)
+
+
+def xq_device_levels(levels: np.ndarray) -> np.ndarray:
+    """The oracle's levels [K/32, B, 2, 32] (positions in XQ_POS order) in the
+    library's device layout [ceil(K/256), B, 2, 4, 8, 8] (item, column, level,
+    position group p/8, block of the item, byte p%8; blocks past K/32 zero)."""
+    nblk, B = levels.shape[:2]
+    ni = -(-nblk // 8)
+    pad = np.zeros((ni * 8, B, 2, 32), dtype=np.int8)
+    pad[:nblk] = levels
+    v = pad.reshape(ni, 8, B, 2, 4, 8)          # item, block-of-item, col, level, group, byte
+    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5))

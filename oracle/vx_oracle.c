@@ -618,3 +618,64 @@ int orc_quantize(uint32_t qtype, const float* x, uint32_t M, uint32_t K, uint64_
     }
     return 0;
 }
+
+/* ------------------------------------------------------ activation split */
+/* The activation format of the library's batched GEMV (vx_quantize_x in
+ * include/vortx_hip.h; no reference counterpart: vortx has no quantized
+ * path). Column b of x [K, B], 32-element block j, v[i] = x[32 j + i, b]:
+ *   m  = max_i |v_i|
+ *   s4[q] = (v[4q] + v[4q+1]) + (v[4q+2] + v[4q+3])          q = 0..7
+ *   S  = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]))
+ *   fin = m < inf and S == S
+ *   c1 = m / 126, c2 = c1 / 254, i1 = (fin and m >= 2^-100) ? 126 / m : 0,
+ *   i2 = i1 * 254 (every operation one IEEE rounding)
+ *   q1_i = clamp(rne(v_i * i1), -127, 127),  r_i = fma(-q1_i, c1, v_i),
+ *   q2_i = clamp(rne(r_i * i2), -127, 127)   (rne of the exact product)
+ *   (a non-finite block stores q1 = q2 = 0)
+ * so x ~= c2 (254 q1 + q2) with |error| <= ~c2 / 2 = max|v| / 64008.
+ * Storage: levels int8 [K/32][B][2][32], element i of the block at byte
+ * position p(i) = 8 (i / 4) + i % 4 for i < 16 and 8 ((i - 16) / 4) + 4 +
+ * (i - 16) % 4 for i >= 16 (the order in which a 32-block's nibbles sit in
+ * a Q4_0 block's 16 bytes: byte t holds elements t and t + 16); scales f32
+ * [K/32][B][2] = {fin ? c2 : m + S, S}. */
+int orc_quantize_x(const float* x, int64_t xs_k, int64_t xs_b, uint32_t K, uint32_t B, int8_t* levels,
+                   float* scales) {
+    if (K % 32) return -2;
+    const uint32_t nblk = K / 32;
+    for (uint32_t j = 0; j < nblk; ++j) {
+        for (uint32_t b = 0; b < B; ++b) {
+            float v[32];
+            for (int i = 0; i < 32; ++i) v[i] = x[(int64_t)(32 * j + i) * xs_k + (int64_t)b * xs_b];
+            float m = 0.0f;
+            for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
+            float s4[8];
+            for (int q = 0; q < 8; ++q) s4[q] = (v[4 * q] + v[4 * q + 1]) + (v[4 * q + 2] + v[4 * q + 3]);
+            const float S = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]));
+            const int fin = m < INFINITY && S == S;
+            const float c1 = m / 126.0f, c2 = c1 / 254.0f;
+            const float i1 = (fin && m >= 0x1p-100f) ? 126.0f / m : 0.0f, i2 = i1 * 254.0f;
+            int8_t* l1 = levels + ((size_t)j * B + b) * 64;
+            int8_t* l2 = l1 + 32;
+            for (int i = 0; i < 32; ++i) {
+                const int p = i < 16 ? 8 * (i / 4) + i % 4 : 8 * ((i - 16) / 4) + 4 + (i - 16) % 4;
+                float q1 = 0.0f, q2 = 0.0f;
+                if (fin) {
+                    /* fmaf(p, s, 1.5 * 2^23) - 1.5 * 2^23 is the exact product p s
+                     * rounded once to the nearest integer, ties to even (|p s|
+                     * stays below ~127, far inside the 2^22 range of the trick) */
+                    q1 = fmaf(v[i], i1, 12582912.0f) - 12582912.0f;
+                    q1 = q1 < -127.0f ? -127.0f : q1 > 127.0f ? 127.0f : q1;
+                    const float r = fmaf(-q1, c1, v[i]);
+                    q2 = fmaf(r, i2, 12582912.0f) - 12582912.0f;
+                    q2 = q2 < -127.0f ? -127.0f : q2 > 127.0f ? 127.0f : q2;
+                }
+                l1[p] = (int8_t)q1;
+                l2[p] = (int8_t)q2;
+            }
+            float* sc = scales + ((size_t)j * B + b) * 2;
+            sc[0] = fin ? c2 : m + S;
+            sc[1] = S;
+        }
+    }
+    return 0;
+}

@@ -73,20 +73,21 @@ def test_tiled_parity(gemm, M, N, K):
 
 @pytest.mark.parametrize("M,N,K,tr_b", [(67, 33, 17, False), (128, 256, 16, False), (129, 257, 31, True),
                                         (300, 517, 129, False), (513, 1000, 100, True), (1024, 1024, 1024, False)])
-def test_wide_tiles_match_narrow(gemm, M, N, K, tr_b, monkeypatch):
+def test_wide_tiles_match_narrow(gemm, M, N, K, tr_b):
     """The 128 x 256 tile kernels (chosen for shapes such as 4096^3, forced
-    here with VX_GEMM_WIDE=1) give the same bits as the 128 x 128 ones: each
-    output is the same sum in the same order. Edge tiles in M, N and K."""
+    here with VX_GEMM_TILE_WIDE) give the same bits as the 128 x 128 ones
+    (VX_GEMM_TILE_NARROW) and as the default choice: each output is the same
+    sum in the same order. Edge tiles in M, N and K."""
     note(f"wide tiles {M}x{N}x{K} trB={tr_b}")
     a = S.uniform((M, K), 5, DEV)
     b = S.uniform((N, K), 6, DEV).t() if tr_b else S.uniform((K, N), 6, DEV)
-    c0, c1 = _nan(M, N), _nan(M, N)
-    monkeypatch.setenv("VX_GEMM_WIDE", "0")
-    gemm.dispatch(c0, a, b)
-    monkeypatch.setenv("VX_GEMM_WIDE", "1")
-    gemm.dispatch(c1, a, b)
+    c0, c1, c2 = _nan(M, N), _nan(M, N), _nan(M, N)
+    gemm.dispatch_ex(c0, a, b, tile="narrow")
+    gemm.dispatch_ex(c1, a, b, tile="wide")
+    gemm.dispatch(c2, a, b)
     torch.cuda.synchronize()
     assert torch.equal(c0.view(torch.int32), c1.view(torch.int32))
+    assert torch.equal(c0.view(torch.int32), c2.view(torch.int32))
     assert_close(c1.cpu().numpy(), _f64(a, b.contiguous())[0, 0])
 
 

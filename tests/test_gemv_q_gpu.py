@@ -188,29 +188,26 @@ def test_gemv_batched_x_edge_values(qgemv, qtype, B):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
-@pytest.mark.parametrize("path", ["simt", "f32", "rows", "rows-f32"])
-def test_gemv_alternate_kernels(qgemv, qtype, path, monkeypatch):
-    """The exact-f32 kernels (VX_GEMV_X_F32 at every batch size, or
-    VX_GEMV_BATCHED=simt for batches) and the per-row-group batch-1 kernels
-    (VX_GEMV_B1=rows, int8 or f32 x) stay selectable. The f32-x kernels
+@pytest.mark.parametrize("path", ["f32", "rows", "rows-f32"])
+def test_gemv_alternate_kernels(qgemv, qtype, path):
+    """The exact-f32 kernels (VX_GEMV_X_F32, every batch size) and the
+    per-row-group batch-1 kernels that take over when x does not fit the
+    persistent kernel's LDS (K > 16384; int8 or f32 x). The f32-x kernels
     accumulate in f32 only and are held to 1e-5."""
-    M, K = 131, 4096
+    M = 131
+    K = 16640 if path.startswith("rows") else 4096
     x_f32 = path in ("f32", "rows-f32")
-    if path == "simt":
-        monkeypatch.setenv("VX_GEMV_BATCHED", "simt")
-    if path.startswith("rows"):
-        monkeypatch.setenv("VX_GEMV_B1", "rows")
-    Bs = [1] if path.startswith("rows") else [1, 2, 4, 8, 16] if path == "f32" else [2, 4, 8, 16]
+    Bs = [1] if path.startswith("rows") else [1, 2, 4, 8, 16]
     w = S.quant_weights(qtype, M, K, seed=31, device=DEV)
     wn = w.cpu().numpy()
     for B in Bs:
-        note(f"gemv {path} {QN[qtype]} B={B}")
+        note(f"gemv {path} {QN[qtype]} K={K} B={B}")
         x = S.activations(B, K, seed=32 + B, device=DEV)
         y = torch.full((B, M), float("nan"), device=DEV)
         qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t(), x_f32=x_f32)
         torch.cuda.synchronize()
         ref = O.gemv_q_f64(qtype, wn, M, K, x.cpu().numpy())
-        tol = 1e-5 if (x_f32 or path == "simt") else 1e-4
+        tol = 1e-5 if x_f32 else 1e-4
         assert_close(y.cpu().numpy().T, ref, tol=tol, what=f"{path} B={B}")
 
 
@@ -305,21 +302,16 @@ def test_non_finite_x_reaches_its_column_only(qgemv, qtype, B, bad):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
-@pytest.mark.parametrize("path", ["k-large", "rows", "rows-f32", "x-f32", "simt"])
+@pytest.mark.parametrize("path", ["k-large", "k-large-f32", "x-f32", "batched-f32"])
 @pytest.mark.parametrize("bad", [float("nan"), float("inf")], ids=["nan", "inf"])
-def test_non_finite_x_other_paths(qgemv, qtype, path, bad, monkeypatch):
+def test_non_finite_x_other_paths(qgemv, qtype, path, bad):
     """The same on the other routes: batch 1 with K > 16384 (the per-row-group
-    int8 kernels by default), VX_GEMV_B1=rows with int8 or f32 x, f32 x at
-    batch 1 (VX_GEMV_X_F32) and the exact-f32 batched kernels
-    (VX_GEMV_BATCHED=simt)."""
+    kernels, int8 or f32 x), f32 x at batch 1 (VX_GEMV_X_F32) and the
+    exact-f32 batched kernels (VX_GEMV_X_F32 with B = 3)."""
     M = 96
-    K = 16640 if path == "k-large" else 2048
-    B = 3 if path == "simt" else 1
-    if path in ("rows", "rows-f32"):
-        monkeypatch.setenv("VX_GEMV_B1", "rows")
-    if path == "simt":
-        monkeypatch.setenv("VX_GEMV_BATCHED", "simt")
-    x_f32 = path in ("rows-f32", "x-f32")
+    K = 16640 if path.startswith("k-large") else 2048
+    B = 3 if path == "batched-f32" else 1
+    x_f32 = path != "k-large"
     note(f"gemv non-finite x {QN[qtype]} path={path} {bad}")
     w = vx.QWeight(S.quant_weights(qtype, M, K, seed=5, device=DEV), qtype, M, K)
     x = S.activations(B, K, seed=6, device=DEV)

@@ -1,0 +1,153 @@
+"""The oracle's activation split (orc_quantize_x), pinned without the GPU.
+
+x is split per 32-element block into two int8 levels with one scale,
+x ~= c2 (254 q1 + q2). Nothing in the reference covers this (vortx has no
+quantized path), so it is pinned by what the mathematics fixes: exact
+recovery of inputs the format represents, the error bound, equivariance under
+powers of two and sign, the element order tied to the Q4_0 nibble layout,
+and the non-finite / tiny-block rules.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+# c2 / 2 relative to the block's max|x| (c2 = max / (126 * 254)), plus the
+# roundings of the scales: 254 c2 differs from c1 by <= 2^-24 c1 (times |q1| <= 126)
+# and i2 c2 from 1 by a few 2^-24 (times |q2| <= 127): < 1e-3 of c2 / 2 together.
+BOUND = 1.0 / 64008.0 * (1 + 1e-3)
+
+
+def _split(x):
+    lv, sc = O.quantize_x(np.asarray(x, dtype=np.float32))
+    return lv, sc
+
+
+def test_position_order_is_the_q4_0_nibble_order():
+    """Position p of a level array holds the element whose nibble sits at p in
+    the pair (low nibbles of dword g, high nibbles of dword g) of a Q4_0
+    block's 16 bytes: byte t holds elements t (low) and t + 16 (high)."""
+    pos_from_layout = np.empty(32, dtype=int)
+    for g in range(4):
+        for t in range(4):
+            byte = 4 * g + t
+            pos_from_layout[byte] = 8 * g + t           # low nibble of byte -> element `byte`
+            pos_from_layout[byte + 16] = 8 * g + 4 + t  # high nibble -> element byte + 16
+    assert np.array_equal(O.XQ_POS, pos_from_layout)
+    assert sorted(O.XQ_POS) == list(range(32))
+    for i in range(32):  # one-hot blocks land at their position
+        x = np.zeros((1, 32), np.float32)
+        x[0, i] = 3.0
+        lv, _ = _split(x)
+        assert lv[0, 0, 0, O.XQ_POS[i]] == 126 and np.count_nonzero(lv) == 1
+
+
+def test_exact_grid_is_recovered():
+    """With max|x| = 126 the scales are c1 = 1, i1 = 1, i2 = 254: x = a + k/256
+    (exact in f32) splits into q1 = a and q2 = the nearest integer to 254 k / 256,
+    ties to even (k = 64: 63.5 -> 64, k = -64: -63.5 -> -64, k = 192: 190.5 is
+    past |r| < 1/2 so it is never used)."""
+    rng = np.random.default_rng(3)
+    a = rng.integers(-125, 126, 32)
+    k = rng.integers(-127, 128, 32)
+    k[:6] = [64, -64, 32, 0, 127, -127]
+    a[31] = 126
+    k[31] = 0  # the block max (every other |x| < 125.5)
+    x = (a + k / 256.0).astype(np.float32)
+    assert np.array_equal(x.astype(np.float64), a + k / 256.0)
+    lv, sc = _split(x[None, :])
+    q1 = lv[0, 0, 0, O.XQ_POS]
+    q2 = lv[0, 0, 1, O.XQ_POS]
+    assert np.array_equal(q1, a)
+    expect_q2 = np.rint(254.0 * k / 256.0)  # numpy rounds half to even
+    assert np.array_equal(q2, expect_q2)
+    assert q2[0] == 64 and q2[1] == -64 and q2[2] == 32  # 63.5 -> 64, -63.5 -> -64, 31.75 -> 32
+    assert sc[0, 0, 0] == np.float32(np.float32(126.0 / 126.0) / np.float32(254.0))
+    assert sc[0, 0, 1] == np.float32(x.astype(np.float64).sum())  # integer-grid sum: exact
+
+
+@pytest.mark.parametrize("dist", ["normal", "uniform", "heavy", "ties"])
+def test_error_bound(dist):
+    rng = np.random.default_rng(11)
+    B, K = 5, 32 * 64
+    if dist == "normal":
+        x = rng.standard_normal((B, K))
+    elif dist == "uniform":
+        x = rng.uniform(-1, 1, (B, K)) * 10.0 ** rng.integers(-20, 20, (B, K // 32)).repeat(32, 1)
+    elif dist == "heavy":
+        x = rng.standard_cauchy((B, K))
+    else:  # values at half-level boundaries of the first split
+        m = 126.0
+        x = (rng.integers(-125, 126, (B, K)) + 0.5) * (m / 126.0)
+        x[:, ::32] = m
+    x = x.astype(np.float32)
+    lv, sc = _split(x)
+    xr = O.xq_decode_f64(lv, sc)
+    bm = np.abs(x.reshape(B, -1, 32)).max(-1, keepdims=True).astype(np.float64)
+    rel = (np.abs(xr - x).reshape(B, -1, 32) / bm).max()
+    assert rel <= BOUND, rel
+
+
+def test_power_of_two_and_sign_equivariance():
+    """Every step is a ratio or a product of ratios of x, so scaling x by 2^e
+    scales c2 and S by 2^e and leaves the levels; -x negates levels and S."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    lv, sc = _split(x)
+    for e in (-40, -7, 9, 60):
+        lv2, sc2 = _split(x * np.float32(2.0 ** e))
+        assert np.array_equal(lv2, lv)
+        assert np.array_equal(sc2, sc * np.float32(2.0 ** e))
+    lvn, scn = _split(-x)
+    assert np.array_equal(lvn, -lv)
+    assert np.array_equal(scn[..., 0], sc[..., 0]) and np.array_equal(scn[..., 1], -sc[..., 1])
+
+
+def test_sum_is_the_stated_tree():
+    """S adds the 32 values as a fixed tree (pairs inside each 4, then the 8
+    partial sums pairwise); a block where sequential summation cancels
+    differently tells the orders apart."""
+    v = np.array([1e8, 1, -1e8, 1] * 8, dtype=np.float32)
+    v[5] = 3
+    _, sc = _split(v[None, :])
+    s4 = [(v[4 * q] + v[4 * q + 1]) + (v[4 * q + 2] + v[4 * q + 3]) for q in range(8)]
+    tree = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]))
+    seq = np.float32(0)
+    for t in v:
+        seq = np.float32(seq + t)
+    assert sc[0, 0, 1] == tree and tree != seq
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_non_finite_block(bad):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((2, 128)).astype(np.float32)
+    ref_lv, ref_sc = _split(x)
+    x[0, 40] = bad
+    lv, sc = _split(x)
+    assert not np.isfinite(sc[1, 0, 0]) and (lv[1, 0] == 0).all()  # block 1 of column 0
+    other = np.ones(sc.shape[:2], bool)
+    other[1, 0] = False
+    assert np.array_equal(lv[other], ref_lv[other]) and np.array_equal(sc[other], ref_sc[other])
+
+
+def test_tiny_and_zero_blocks():
+    x = np.zeros((1, 96), np.float32)
+    x[0, 32:64] = np.float32(2.0 ** -110) * np.arange(1, 33, dtype=np.float32)
+    x[0, 64:96] = np.float32(2.0 ** -99)
+    lv, sc = _split(x)
+    assert (lv[0:2] == 0).all()                       # zero block and one below 2^-100: no levels
+    assert sc[1, 0, 1] == np.float32(2.0 ** -110 * 528)  # S still exact
+    assert (lv[2, 0, 0] == 126).all()                 # 2^-99 is split normally
+    assert sc[0, 0, 0] == 0 and sc[0, 0, 1] == 0
+
+
+def test_strided_input_matches_contiguous():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    lv, sc = _split(x)
+    xt = np.ascontiguousarray(x.T)  # [K, B] storage: xs_k = B, xs_b = 1
+    levels = np.zeros_like(lv)
+    scales = np.zeros_like(sc)
+    assert O.lib().orc_quantize_x(xt.ctypes.data, 4, 1, 256, 4, levels.ctypes.data, scales.ctypes.data) == 0
+    assert np.array_equal(levels, lv) and np.array_equal(scales, sc)

@@ -28,7 +28,7 @@ from . import _ffi
 from ._ffi import (NONE_STRIDE, ROUTE_EMPTY, ROUTE_GEMV, ROUTE_NAIVE, ROUTE_TILED, VX_Q4_0, VX_Q4_K, VX_Q8_0,
                    VortxError, check, lib)
 
-__all__ = ["TensorLayout", "layout_extent", "Gemm", "QuantGemv", "QWeight", "Contiguous", "GGUFFile", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
+__all__ = ["TensorLayout", "layout_extent", "XQ", "xq_size", "Gemm", "QuantGemv", "QWeight", "Contiguous", "GGUFFile", "VortxError", "VX_Q4_0", "VX_Q8_0", "VX_Q4_K",
            "ROUTE_NAIVE", "ROUTE_TILED", "ROUTE_GEMV", "ROUTE_EMPTY", "qtype_info", "lib"]
 
 # Load eagerly: a missing library must fail at import, not at first call.
@@ -196,12 +196,16 @@ class Gemm(_Context):
         self._call(lib().vx_gemm_f32, out, lhs, rhs, stream)
 
     def dispatch_ex(self, out, lhs, rhs, alpha: float = 1.0, beta: float = 0.0, broadcast: bool = False,
-                    stream=None) -> None:
+                    tile: str = "auto", stream=None) -> None:
         """out = alpha * (lhs x rhs) + beta * out (vx_gemm_f32_ex); out is not
         read when beta == 0. ``broadcast``: batch dims of lhs / rhs of size 1
-        are reused along out's (src/shapes.rs:346-391 semantics)."""
+        are reused along out's (src/shapes.rs:346-391 semantics). ``tile``:
+        "narrow" / "wide" pins the MFMA kernel's 128 x 128 / 128 x 256 output
+        tiles (same bits either way), "auto" lets the library choose."""
         o, l, r = _view_of(out, True), _view_of(lhs, False), _view_of(rhs, False)
-        opts = _ffi.VxGemmOpts(alpha, beta, _ffi.VX_GEMM_BROADCAST if broadcast else 0, 0)
+        flags = (_ffi.VX_GEMM_BROADCAST if broadcast else 0) | {"auto": 0, "narrow": _ffi.VX_GEMM_TILE_NARROW,
+                                                                 "wide": _ffi.VX_GEMM_TILE_WIDE}[tile]
+        opts = _ffi.VxGemmOpts(alpha, beta, flags, 0)
         check(lib().vx_gemm_f32_ex(self._h, _stream(stream), C.byref(o), C.byref(l), C.byref(r), C.byref(opts)))
 
     def dispatch_naive(self, out, lhs, rhs, stream=None) -> None:
@@ -260,8 +264,66 @@ class QWeight:
         return w
 
 
+def xq_size(K: int, B: int) -> int:
+    """Bytes of the activation split of a [K, B] x (include/vortx_hip.h vx_xq)."""
+    n = C.c_uint64()
+    check(lib().vx_xq_size(K, B, C.byref(n)))
+    return n.value
+
+
+@dataclass
+class XQ:
+    """x [K, B] split into two int8 levels per 32-block (vx_xq): a uint8 GPU
+    buffer of at least xq_size(K, B) bytes, 16-byte aligned. ``levels()``
+    views its level bytes in the device layout ([ceil(K/256), B, 2, 4, 8, 8]
+    int8: item, column, level, position group, block of the item, byte) and
+    ``scales()`` its [K/32, B, 2] f32 scales."""
+    data: object
+    K: int
+    B: int
+
+    def __post_init__(self):
+        need = xq_size(self.K, self.B)
+        have = self.data.numel() * self.data.element_size()
+        if have < need:
+            raise VortxError(_ffi.VX_ERR_INVALID, f"XQ needs {need} bytes, the buffer holds {have}")
+
+    @staticmethod
+    def empty(K: int, B: int, device="cuda:0") -> "XQ":
+        import torch
+        return XQ(torch.empty(xq_size(K, B), dtype=torch.uint8, device=device), K, B)
+
+    def levels(self):
+        import torch
+        ni = (self.K + 255) // 256
+        return self.data[:ni * self.B * 512].view(torch.int8).view(ni, self.B, 2, 4, 8, 8)
+
+    def scales(self):
+        import torch
+        ni, nb = (self.K + 255) // 256, self.K // 32
+        off = ni * self.B * 512
+        return self.data[off:off + nb * self.B * 8].view(torch.float32).view(nb, self.B, 2)
+
+    def _c(self) -> _ffi.VxXq:
+        q = _ffi.VxXq()
+        q.base = self.data.data_ptr()
+        q.K = self.K
+        q.B = self.B
+        return q
+
+
 class QuantGemv(_Context):
     """y = W x for GGML Q8_0 / Q4_0 / Q4_K weights, f32 accumulate."""
+
+    def quantize_x(self, out: XQ, x, stream=None) -> None:
+        """Split x (a [K, B] f32 view, or [K]) into ``out`` (vx_quantize_x)."""
+        xv, q = _view_of(x, False), out._c()
+        check(lib().vx_quantize_x(self._h, _stream(stream), C.byref(q), C.byref(xv)))
+
+    def dispatch_xq(self, y, w: "QWeight", xq: XQ, stream=None) -> None:
+        """y = W x from the split of x (vx_gemv_q_xq)."""
+        yv, wc, q = _view_of(y, True), w._c(), xq._c()
+        check(lib().vx_gemv_q_xq(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(q)))
 
     def dispatch(self, y, w: QWeight, x, stream=None, x_f32: bool = False, x_int8: bool = False) -> None:
         """y = W x. By default x is split per 32-block into two int8 levels

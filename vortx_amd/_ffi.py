@@ -36,11 +36,15 @@ class VxQWeight(C.Structure):
                 ("reserved", C.c_uint32), ("row_stride_bytes", C.c_uint64)]
 
 
+class VxXq(C.Structure):
+    _fields_ = [("base", C.c_void_p), ("K", C.c_uint32), ("B", C.c_uint32)]
+
+
 class VxGemmOpts(C.Structure):
     _fields_ = [("alpha", C.c_float), ("beta", C.c_float), ("flags", C.c_uint32), ("reserved", C.c_uint32)]
 
 
-VX_GEMM_BROADCAST = 1
+VX_GEMM_BROADCAST, VX_GEMM_TILE_NARROW, VX_GEMM_TILE_WIDE = 1, 2, 4
 
 
 class VxGgufHeader(C.Structure):
@@ -74,6 +78,9 @@ SIGNATURES = [
     ("vx_gemv_q", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView)]),
     ("vx_gemv_q_ex", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView), C.c_uint32]),
     ("vx_dequantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight)]),
+    ("vx_xq_size", C.c_int, [C.c_uint32, C.c_uint32, _P(C.c_uint64)]),
+    ("vx_quantize_x", C.c_int, [C.c_void_p, C.c_void_p, _P(VxXq), _P(VxCView)]),
+    ("vx_gemv_q_xq", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxXq)]),
     ("vx_quantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxQWeight), _P(VxCView)]),
     ("vx_contiguous", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), C.c_void_p]),
     ("vx_qtype_info", C.c_int, [C.c_uint32, _P(C.c_uint32), _P(C.c_uint32)]),

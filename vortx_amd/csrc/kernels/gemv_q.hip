@@ -165,8 +165,8 @@ __device__ __forceinline__ void vx_gemv_b1(const vx_gemv_args& a) {
 // full queue; the rest of a deeper ring is issued after it. The two 32-block sums of
 // x per unit (for the offset terms of vx_unit_dot_b1) are reduced in the
 // staging step with lane shuffles, so no second barrier is needed.
-// WGT = 1024: 16 waves of at most 128 VGPRs; 512: 8 waves with room for a
-// deeper ring. x must fit VX_P_XF float4 (K <= 16384).
+// WGT = 1024: 16 waves of at most 128 VGPRs. x must fit VX_P_XF float4
+// (K <= 16384).
 #define VX_P_XF 4096u
 
 template <int QT, int P, int WGT, bool XV>
@@ -1222,15 +1222,10 @@ VX_GEMV_ALL(VX_Q4_K, q4_k)
 VX_GEMV_P1(VX_Q4_0, q4_0, 2, 1024)
 VX_GEMV_P1(VX_Q8_0, q8_0, 1, 1024)
 VX_GEMV_P1(VX_Q4_K, q4_k, 2, 1024)
-VX_GEMV_P1(VX_Q4_0, q4_0, 4, 512)
-VX_GEMV_P1(VX_Q8_0, q8_0, 3, 512)
-VX_GEMV_P1(VX_Q4_K, q4_k, 4, 512)
 VX_GEMV_P1I(VX_Q4_0, q4_0, 2)
-VX_GEMV_P1I(VX_Q4_0, q4_0, 3)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
-VX_GEMV_P1I(VX_Q4_K, q4_k, 3)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 1)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 2)
 VX_GEMV_I8B(VX_Q4_0, q4_0, 4)
@@ -1240,3 +1235,424 @@ VX_GEMV_I8B(VX_Q8_0, q8_0, 4)
 VX_GEMV_I8B(VX_Q4_K, q4_k, 1)
 VX_GEMV_I8B(VX_Q4_K, q4_k, 2)
 VX_GEMV_I8B(VX_Q4_K, q4_k, 4)
+
+// ------------------------------------------------------------------------
+// Batched GEMV on split activations (vx_xq, written once per call by
+// vx_quantize_x: two int8 levels and {c2, S} per 32-block and column, the
+// levels in the order of a Q4_0 block's nibbles) on the int8 matrix cores,
+// one v_mfma_i32_16x16x32_i8 per 32-block and group of 8 columns:
+//   A (16 x 32): row i = 2 c + L is level L of column 8 h + c; lane (i, g)
+//     holds bytes 8g..8g+7 of that block's level array;
+//   B (32 x 16): column n is W row n of the 16-row tile; lane (n, g) holds
+//     the 8 weights those bytes pair with: the low then the high nibbles of
+//     qs dword g (Q4_0), qs dwords g and 4 + g (Q8_0), the low or high
+//     nibbles of qs-chunk dwords g and 4 + g (Q4_K sub-block 2c or 2c + 1);
+//   D (16 x 16): lane (n, g) receives rows 4g..4g+3, columns 8h + 2g and
+//     8h + 2g + 1 with both levels, of W row n, T = 254 D_L0 + D_L1 (exact
+//     int32, |D| < 2^20), and applies the block's scales in f32:
+//       Q4_0  acc += d (c2 T - 8 S)       (nibbles used unbiased)
+//       Q8_0  acc += d (c2 T)
+//       Q4_K  acc += (d sc) (c2 T) - (dmin m) S
+// Work split: one workgroup of 16 waves per CU (grid = CU count); CU c owns
+// the 16-row tiles c, c + G, ...; wave w owns the K slice s = (w + c) mod 16:
+// items (256 weights) s, s + 16, ... up to XI per pass. The rotation by c
+// keeps the waves of the chip from reading the same slice of x at the same
+// time. A wave loads its slice's x levels into registers once per pass and
+// reuses them for every tile; per tile it streams 16 rows x 256 weights per
+// item, lane (n, u) loading quarter u of row n's item (a unit of 64 weights,
+// or the Q4_K super-block's header and qs chunk u) with 16-byte loads, and
+// 4 x 4 transposes across the four 16-lane rows (v_permlane32_swap +
+// v_permlane16_swap) turn quarters into the per-block MFMA layout. Weight
+// items flow through a ring of R = XI * TU register slots (TU = 2 tiles when
+// XI = 1). At the end of each tile the 16 waves' partial sums meet in LDS and
+// one thread per output adds them in slice order (deterministic), adding to
+// its own y of the previous passes when K takes several passes.
+
+// v_permlane{16,32}_swap results pass through empty asm: see vx_pin2.
+__device__ __forceinline__ void vx_swap32(uint32_t& x, uint32_t& y) {
+    vx_pin2(x, y);
+    const auto s = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+    x = s[0];
+    y = s[1];
+    vx_pin2(x, y);
+}
+__device__ __forceinline__ void vx_swap16(uint32_t& x, uint32_t& y) {
+    vx_pin2(x, y);
+    const auto s = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+    x = s[0];
+    y = s[1];
+    vx_pin2(x, y);
+}
+
+// 4 x 4 transpose across the 16-lane rows: on entry row u of r[k] holds
+// A[u][k]; on exit row g of r[k] holds A[k][g]. permlane32_swap(x, y)
+// exchanges rows 2, 3 of x with rows 0, 1 of y; permlane16_swap(x, y) rows
+// 1, 3 of x with rows 0, 2 of y.
+__device__ __forceinline__ void vx_t4(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    vx_swap32(r0, r2);  // r0 = [A00 A10 A02 A12], r2 = [A20 A30 A22 A32]
+    vx_swap32(r1, r3);  // r1 = [A01 A11 A03 A13], r3 = [A21 A31 A23 A33]
+    vx_swap16(r0, r1);  // r0 = [A00 A01 A02 A03], r1 = [A10 A11 A12 A13]
+    vx_swap16(r2, r3);  // r2 = [A20 A21 A22 A23], r3 = [A30 A31 A32 A33]
+}
+
+// Every row's value of v in every lane: o[u] = v of 16-lane row u.
+__device__ __forceinline__ void vx_gather4(uint32_t v, uint32_t (&o)[4]) {
+    uint32_t a = v, b = v;
+    vx_swap32(a, b);  // a = [v0 v1 v0 v1], b = [v2 v3 v2 v3]
+    uint32_t a2 = a, b2 = b;
+    vx_swap16(a, a2);  // a = [v0 v0 v0 v0], a2 = [v1 v1 v1 v1]
+    vx_swap16(b, b2);  // b = [v2 v2 v2 v2], b2 = [v3 v3 v3 v3]
+    o[0] = a;
+    o[1] = a2;
+    o[2] = b;
+    o[3] = b2;
+}
+
+// The weights of one item (8 blocks / sub-blocks of 32) in MFMA layout.
+template <int QT>
+struct vx_xq_item {
+    uint32_t lo[8], hi[8];  // B operand of block b: lo[b] | hi[b] << 32 (int8 lanes)
+    float ds[8];            // d of block b, this lane's row (Q4_0, Q8_0)
+    uint32_t scm[4];        // Q4_K: sub-blocks 2k, 2k + 1: bytes sc, m, sc, m (6-bit)
+    float d, dmin;          // Q4_K super-block scales
+    // Q4_K: d sc and -dmin m of sub-block b
+    __device__ __forceinline__ float dsc(int b) const {
+        return d * (float)((scm[b >> 1] >> (16 * (b & 1))) & 0xFFu);
+    }
+    __device__ __forceinline__ float dmm(int b) const {
+        return -(dmin * (float)((scm[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu));
+    }
+};
+
+template <int QT>
+__device__ __forceinline__ void vx_xq_prepare(uint32_t (&r)[vx_unit<QT>::NW], uint32_t u, vx_xq_item<QT>& it) {
+    constexpr uint32_t NIB = 0x0F0F0F0Fu;
+    if constexpr (QT == VX_Q4_0) {
+        // unit u = blocks 2u (d in bytes 0-1, qs 2..17) and 2u + 1 (d 18-19, qs 20..35)
+        uint32_t e0 = __builtin_amdgcn_alignbit(r[1], r[0], 16), e1 = __builtin_amdgcn_alignbit(r[2], r[1], 16);
+        uint32_t e2 = __builtin_amdgcn_alignbit(r[3], r[2], 16), e3 = __builtin_amdgcn_alignbit(r[4], r[3], 16);
+        uint32_t o0 = r[5], o1 = r[6], o2 = r[7], o3 = r[8];
+        vx_t4(e0, e1, e2, e3);  // e_k: qs dword g of block 2k
+        vx_t4(o0, o1, o2, o3);  // o_k: qs dword g of block 2k + 1
+        const uint32_t q[8] = {e0, o0, e1, o1, e2, o2, e3, o3};
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            it.lo[b] = vx_and(q[b], NIB);
+            it.hi[b] = vx_and(q[b] >> 4, NIB);
+        }
+        uint32_t dd[4];
+        vx_gather4((r[0] & 0xFFFFu) | (r[4] & 0xFFFF0000u), dd);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            it.ds[2 * k] = vx_f16_to_f32(dd[k]);
+            it.ds[2 * k + 1] = vx_f16_to_f32(dd[k] >> 16);
+        }
+    } else if constexpr (QT == VX_Q8_0) {
+        // unit u = blocks 2u (d 0-1, qs 2..33) and 2u + 1 (d 34-35, qs 36..67)
+        uint32_t a[8], b[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            a[k] = __builtin_amdgcn_alignbit(r[k + 1], r[k], 16);
+            b[k] = r[9 + k];
+        }
+        vx_t4(a[0], a[1], a[2], a[3]);  // a[k]: dword g of block 2k
+        vx_t4(a[4], a[5], a[6], a[7]);  // a[4 + k]: dword 4 + g of block 2k
+        vx_t4(b[0], b[1], b[2], b[3]);
+        vx_t4(b[4], b[5], b[6], b[7]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            it.lo[2 * k] = a[k];
+            it.hi[2 * k] = a[4 + k];
+            it.lo[2 * k + 1] = b[k];
+            it.hi[2 * k + 1] = b[4 + k];
+        }
+        uint32_t dd[4];
+        vx_gather4((r[0] & 0xFFFFu) | (r[8] & 0xFFFF0000u), dd);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            it.ds[2 * k] = vx_f16_to_f32(dd[k]);
+            it.ds[2 * k + 1] = vx_f16_to_f32(dd[k] >> 16);
+        }
+    } else {
+        // header r[0..3] (d, dmin, 12 scale bytes), qs chunk u in r[4..11]:
+        // sub-blocks 2u (low nibbles) and 2u + 1 (high nibbles)
+        uint32_t c0 = r[4], c1 = r[5], c2 = r[6], c3 = r[7];
+        uint32_t c4 = r[8], c5 = r[9], c6 = r[10], c7 = r[11];
+        vx_t4(c0, c1, c2, c3);  // c_k: chunk k dword g
+        vx_t4(c4, c5, c6, c7);  // c_{4+k}: chunk k dword 4 + g
+        const uint32_t lo4[4] = {c0, c1, c2, c3}, hi4[4] = {c4, c5, c6, c7};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            it.lo[2 * k] = vx_and(lo4[k], NIB);
+            it.hi[2 * k] = vx_and(hi4[k], NIB);
+            it.lo[2 * k + 1] = vx_and(lo4[k] >> 4, NIB);
+            it.hi[2 * k + 1] = vx_and(hi4[k] >> 4, NIB);
+        }
+        it.d = vx_f16_to_f32(r[0]);
+        it.dmin = vx_f16_to_f32(r[0] >> 16);
+        // this lane's two sub-blocks' 6-bit (scale, min), packed, then every
+        // chunk's from its row
+        uint32_t sc0, m0, sc1, m1;
+        vx_q4k_scales(r[1], r[2], r[3], u, sc0, m0, sc1, m1);
+        vx_gather4(sc0 | (m0 << 8) | (sc1 << 16) | (m1 << 24), it.scm);
+    }
+}
+
+#define VX_XQ_WG 1024
+typedef long i64x2 __attribute__((ext_vector_type(2)));
+
+// LDS of vx_gemv_xq: per wave, the scales of its K slice in the current
+// pass [8 XI blocks][CP columns] float2 {c2, S'} (S' = -8 S for Q4_0); then
+// red[RMAX tiles][16 slots][CP][16 rows] partial sums.
+// Schedule (measured with per-wave s_memrealtime stamps): the chip's weight
+// requests go out together, so their data returns in no useful order; a
+// barrier per tile then waits for the last wave's item, by which time most of
+// the matrix has arrived, and the compute runs after the stream instead of
+// under it. So nothing here waits for other waves while streaming:
+//  1. each wave loads its slice's x levels (registers) and scales (its own
+//     LDS region) and waits for them alone; x goes out before the weights,
+//     as an x request behind the chip's weight requests returns late;
+//  2. then its ring of weight items; each item is reduced as it arrives and
+//     its partial sums parked in red[tile-work mod RMAX];
+//  3. every RMAX tile-works (for the usual shapes once, at the end) the
+//     workgroup meets, one thread per output adds the 16 slots in slice
+//     order (deterministic) and writes y.
+// Wait counts: inside the streaming loop the only memory loads are the ring
+// refills, issued unconditionally (clamped inside the matrix past the last
+// tile-work) in whole rounds of RD, so each wait covers just its slot. MP
+// (several passes, K past 16 XI items) adds loads of the next pass's x and of
+// y, which makes those waits conservative; it is compiled separately.
+#define VX_XQ_RED_BYTES 65536u
+template <int QT, int NCG, int XI, int RD, bool MP>
+__device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    constexpr uint32_t CP = 8u * NCG;             // columns per launch (padded)
+    constexpr uint32_t PI = 16u * XI;             // items per pass
+    constexpr uint32_t NSW = 8u * XI * CP;        // scale entries per wave and pass
+    constexpr int SPL = (int)((NSW + 63u) / 64u);  // ... per lane
+    constexpr uint32_t TILE_F = 16u * CP * 16u;   // red floats per tile-work
+    constexpr uint32_t RMAX = VX_XQ_RED_BYTES / (TILE_F * 4u);
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t n = lane & 15u, g = lane >> 4;
+    const uint32_t G = gridDim.x, cu = blockIdx.x;
+    const uint32_t ntiles = (a.M + 15u) >> 4;
+    const uint32_t nts = ntiles > cu ? (ntiles - cu + G - 1u) / G : 0u;
+    if (nts == 0u) return;  // uniform over the workgroup
+    const uint32_t slot = (wave + cu) & 15u;
+    const uint32_t B = a.B, nblk = a.nblk, ipr = a.ipr;
+    const uint32_t nwork = (MP ? a.npass : 1u) * nts;  // tile-works over all passes
+
+    float* red = (float*)vx_lds_x;                               // [RMAX][16][CP][16]
+    float2* scl = (float2*)(red + RMAX * TILE_F) + wave * NSW;   // this wave's [8 XI][CP]
+
+    auto row_of = [&](uint32_t ts) { return min((cu + ts * G) * 16u + n, a.M - 1u); };
+    // W loads of tile-work w (clamped to the last one), item j of this wave
+    // (clamped inside the matrix)
+    auto wload = [&](uint32_t w, int j, uint32_t (&r)[NW]) {
+        w = min(w, nwork - 1u);
+        const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
+        const uint32_t item = min(p * PI + slot + 16u * (uint32_t)j, ipr - 1u);
+        const uint8_t* rp = a.w + (uint64_t)row_of(ts) * a.row_stride;
+        vx_load_unit<QT, true>(rp, min(4u * item + g, a.nunits - 1u), r);
+    };
+    // this wave's x levels and scales of pass p, from clamped addresses.
+    // Nothing here uses the loaded values (lanes of columns >= B or of blocks
+    // past K feed only D rows / MFMAs that are never used; the scales are
+    // masked when they go to LDS), so no wait is forced before the caller's.
+    float2 sv[SPL];
+    long xa[XI][8][NCG];
+    auto pass_loads = [&](uint32_t p) {
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            // entry e = (j, b, col): block 8 (p PI + slot + 16 j) + b
+            const uint32_t e = lane + 64u * (uint32_t)i;
+            const uint32_t jb = e / CP, col = e - jb * CP;
+            const uint32_t blk = 8u * (p * PI + slot + 16u * (jb >> 3)) + (jb & 7u);
+            sv[i] = *(const float2*)(a.scales + 2u * ((uint64_t)min(blk, nblk - 1u) * a.xcols + a.col0 +
+                                                      min(col, B - 1u)));
+        }
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            const uint32_t item = p * PI + slot + 16u * (uint32_t)j;
+#pragma unroll
+            for (int h = 0; h < NCG; ++h) {
+                // lane (i, g): level i % 2 of column 8 h + i / 2, the 8 bytes
+                // of position group g of each of the item's 8 blocks: 64
+                // contiguous bytes (vx_quantize_x's item-major layout)
+                const uint32_t col = 8u * (uint32_t)h + (n >> 1);
+                const uint8_t* lp = (const uint8_t*)a.levels +
+                                    (((uint64_t)min(item, ipr - 1u) * a.xcols + a.col0 + min(col, B - 1u)) * 2u +
+                                     (n & 1u)) * 256u + 64u * g;
+                const i64x2 v0 = *(const i64x2*)lp, v1 = *(const i64x2*)(lp + 16);
+                const i64x2 v2 = *(const i64x2*)(lp + 32), v3 = *(const i64x2*)(lp + 48);
+                xa[j][0][h] = v0.x; xa[j][1][h] = v0.y; xa[j][2][h] = v1.x; xa[j][3][h] = v1.y;
+                xa[j][4][h] = v2.x; xa[j][5][h] = v2.y; xa[j][6][h] = v3.x; xa[j][7][h] = v3.y;
+            }
+        }
+    };
+    // the scales to this wave's LDS region (read back by the same wave only)
+    auto pass_publish = [&](uint32_t p) {
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const uint32_t e = lane + 64u * (uint32_t)i;
+            const uint32_t jb = e / CP, col = e - jb * CP;
+            const uint32_t blk = 8u * (p * PI + slot + 16u * (jb >> 3)) + (jb & 7u);
+            float2 v = (blk < nblk && col < B) ? sv[i] : float2{0.f, 0.f};
+            if constexpr (QT == VX_Q4_0) v.y *= -8.f;
+            if (e < NSW) scl[e] = v;
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): LDS stores done (vmcnt, expcnt untouched)
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    pass_loads(0u);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pass_publish(0u);
+    uint32_t raw[RD * XI][NW];
+#pragma unroll
+    for (int u = 0; u < RD; ++u)
+#pragma unroll
+        for (int j = 0; j < XI; ++j) wload((uint32_t)u, j, raw[u * XI + j]);
+
+    float acc[NCG][2];
+#pragma unroll
+    for (int h = 0; h < NCG; ++h) acc[h][0] = acc[h][1] = 0.f;
+
+    // the workgroup meets and writes y for tile-works [w0, w1]: one thread
+    // per output of each tile in the range, adding the tile's passes in the
+    // range in pass order (with several passes a range can hold one tile more
+    // than once); an earlier range's sum of the tile is read back from y
+    // (written before that range's closing barrier)
+    auto flush = [&](uint32_t w0, uint32_t w1) {
+        __syncthreads();
+        const uint32_t per = B * 16u;
+        const uint32_t ntile = min(w1 - w0 + 1u, nts);  // distinct tiles in the range
+        for (uint32_t e = t; e < ntile * per; e += VX_XQ_WG) {
+            const uint32_t k = e / per, rem = e - k * per;
+            const uint32_t col = rem >> 4, rr = rem & 15u;
+            const uint32_t ts = (w0 + k) % nts;
+            const uint32_t row = (cu + ts * G) * 16u + rr;
+            float* yp = a.y + (int64_t)min(row, a.M - 1u) * a.ys_m + (int64_t)col * a.ys_b;
+            float tot = 0.f;
+            for (uint32_t w = w0 + k; w <= w1; w += nts) {
+                const float* rb = red + (w % RMAX) * TILE_F;
+                float s = 0.f;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) s += rb[((uint32_t)q * CP + col) * 16u + rr];
+                const uint32_t p = MP ? w / nts : 0u;
+                tot = (w == w0 + k) ? ((MP && p > 0u && row < a.M) ? *yp + s : s) : tot + s;
+            }
+            if (row < a.M) *yp = tot;
+        }
+        __syncthreads();
+    };
+
+    uint32_t wflush = 0;  // first tile-work not yet written to y
+    auto tile_work = [&](uint32_t w, int u) {
+        const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
+        if constexpr (MP) {
+            if (ts == 0u && p > 0u) {
+                pass_loads(p);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                pass_publish(p);
+            }
+        }
+        (void)ts;
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            const uint32_t item = p * PI + slot + 16u * (uint32_t)j;
+            uint32_t (&rw)[NW] = raw[u * XI + j];
+            if (item < ipr) {
+                vx_xq_item<QT> it;
+                vx_xq_prepare<QT>(rw, g, it);
+                const uint32_t bl0 = 8u * (uint32_t)j;  // first block of the item in this wave's scales
+                // block b of the item: MFMA per column group, then the scales
+                auto block = [&](int b) {
+                    const long bw = (long)((uint64_t)it.lo[b] | ((uint64_t)it.hi[b] << 32));
+#pragma unroll
+                    for (int h = 0; h < NCG; ++h) {
+                        const i32x4 D = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa[j][b][h], bw, i32x4{0, 0, 0, 0}, 0, 0, 0);
+                        const f32x4 sc = *(const f32x4*)&scl[(bl0 + (uint32_t)b) * CP + 8u * (uint32_t)h + 2u * g];
+#pragma unroll
+                        for (int c = 0; c < 2; ++c) {
+                            const float T = (float)(__mul24(D[2 * c], 254) + D[2 * c + 1]);
+                            const float c2 = c ? sc.z : sc.x, sx = c ? sc.w : sc.y;
+                            float v = acc[h][c];
+                            if constexpr (QT == VX_Q4_0) {
+                                v = __builtin_fmaf(it.ds[b], __builtin_fmaf(c2, T, sx), v);
+                            } else if constexpr (QT == VX_Q8_0) {
+                                v = __builtin_fmaf(it.ds[b], c2 * T, v);
+                            } else {
+                                v = __builtin_fmaf(it.dsc(b), c2 * T, v);
+                                v = __builtin_fmaf(it.dmm(b), sx, v);
+                            }
+                            acc[h][c] = v;
+                        }
+                    }
+                };
+                if (8u * item + 8u <= nblk) {
+                    // a whole item: no branch between the blocks, so the MFMAs
+                    // of later blocks issue while earlier epilogues run
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) block(b);
+                } else {
+                    const uint32_t nb = nblk - 8u * item;  // the partial last item
+#pragma unroll
+                    for (int b = 0; b < 8; ++b)
+                        if ((uint32_t)b < nb) block(b);
+                }
+            }
+            // refill this ring slot with the same item of the tile-work RD
+            // ahead (clamped: past the end the last one again, from cache)
+            wload(w + RD, j, rw);
+        }
+        // park this slot's partial sums; the workgroup reduces every RMAX
+        float* rb = red + (w % RMAX) * TILE_F;
+#pragma unroll
+        for (int h = 0; h < NCG; ++h)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                rb[(slot * CP + 8u * (uint32_t)h + 2u * g + (uint32_t)c) * 16u + n] = acc[h][c];
+                acc[h][c] = 0.f;
+            }
+        if (w + 1u == nwork || w + 1u - wflush == RMAX) {
+            flush(wflush, w);
+            wflush = w + 1u;
+        }
+    };
+    // whole rounds of RD tile-works (every path issues the same loads), then
+    // the last partial round
+    const uint32_t nfull = nwork - nwork % RD;
+    for (uint32_t w0 = 0; w0 < nfull; w0 += RD) {
+#pragma unroll
+        for (int u = 0; u < RD; ++u) tile_work(w0 + (uint32_t)u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < RD - 1; ++u)
+        if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u);
+}
+
+#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, SFX)                                                   \
+    extern "C" __global__ __launch_bounds__(VX_XQ_WG) void vx_gemv_xq_##QN##_c##NCG##_x##XI##SFX(vx_gemv_xq_args a) { \
+        vx_gemv_xq<QT, NCG, XI, RD, MP>(a);                                                             \
+    }
+// (column groups NCG, items per wave and pass XI, ring depth RD in tiles):
+// RD * XI weight items in flight per wave, as many as the registers allow.
+// One pass (K <= 4096 XI): exact waits; _mp: several passes.
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 1, 4, false, )
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 2, 1, false, )
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, false, )
+VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 3, false, )
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, _mp)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 1, 2, false, )
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, false, )
+VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 2, false, )
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 1, 3, false, )
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, false, )
+VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 2, false, )
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, _mp)

@@ -45,6 +45,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_dpp.hpp"
 
 #pragma clang fp contract(off)
 
@@ -397,5 +398,75 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args
                 q[d] = v;
             }
         }
+    }
+}
+
+// ------------------------------------------------------------------------
+// Activation split for the batched GEMV (no reference counterpart): per
+// column b of x [K, B] and 32-element block j, two int8 levels and one scale,
+//   m = max|v|, S = sum v (a fixed tree: pairs within each 4, then 8 lanes),
+//   c1 = m / 126, c2 = c1 / 254, i1 = 126 / m (0 for m < 2^-100 or a
+//   non-finite block), i2 = 254 i1,
+//   q1 = clamp(rne(v i1), +-127), q2 = clamp(rne(fma(-q1, c1, v) i2), +-127),
+// so x ~= c2 (254 q1 + q2), |error| <= ~max|v| / 64008. A block's 32
+// positions hold element i at position 8 (i / 4) + i % 4 (i < 16) or
+// 8 ((i - 16) / 4) + 4 + i % 4 (i >= 16): the order of a Q4_0 block's nibbles
+// (byte t holds elements t and t + 16), so a 32-bit word of Q4_0 nibbles and
+// 8 bytes of x levels line up for the int8 matrix cores. Levels are stored
+// [item = j / 8][b][level][g = position / 8][j % 8][position % 8]: the 8
+// bytes one matrix-core lane needs from each of an item's 8 blocks sit
+// together (64 bytes per lane). Scales [j][b] = {c2, S}; a block with a NaN
+// or inf stores {m + S, S} and zero levels, so every output of its column
+// becomes non-finite.
+// Eight lanes per (j, b), lane t holding elements 4t..4t+3; every operation
+// is one IEEE rounding (no contraction in this file), so the bytes equal
+// the oracle's sequential restatement (orc_quantize_x).
+#define VX_XQ_MAGIC 12582912.0f  // 1.5 * 2^23
+
+extern "C" __global__ __launch_bounds__(256) void vx_quantize_x(vx_xq_args a) {
+    const uint64_t gid = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    const uint64_t grp = gid >> 3;               // (j, b) = (grp / B, grp % B)
+    const uint32_t t = threadIdx.x & 7u;
+    const uint64_t ngrp = (uint64_t)a.nblk * a.B;
+    // every lane takes part in the DPP reductions; lanes past the end load
+    // group 0 and store nothing
+    const bool in = grp < ngrp;
+    const uint64_t gg = in ? grp : 0u;
+    const uint32_t j = (uint32_t)(gg / a.B), b = (uint32_t)(gg - (uint64_t)j * a.B);
+    const int64_t k0 = 32 * (int64_t)j + 4 * (int64_t)t;
+    f32x4q v;
+    if (a.x_vec) {
+        v = *(const f32x4q*)(a.x + (int64_t)b * a.xs_b + k0);
+    } else {
+        const float* p = a.x + (int64_t)b * a.xs_b + k0 * a.xs_k;
+        v = f32x4q{p[0], p[a.xs_k], p[2 * a.xs_k], p[3 * a.xs_k]};
+    }
+    const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float S = vx_sum8((v.x + v.y) + (v.z + v.w));
+    const bool fin = m < __builtin_inff() && S == S;
+    const float c1 = m / 126.0f, c2 = c1 / 254.0f;
+    const float i1 = (fin && m >= 0x1p-100f) ? 126.0f / m : 0.0f, i2 = i1 * 254.0f;
+    uint32_t w1 = 0, w2 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float t1 = fin ? __builtin_fmaf(v[e], i1, VX_XQ_MAGIC) : VX_XQ_MAGIC;
+        t1 = fminf(fmaxf(t1, VX_XQ_MAGIC - 127.0f), VX_XQ_MAGIC + 127.0f);
+        const float q1 = t1 - VX_XQ_MAGIC;  // exact
+        const float r = __builtin_fmaf(-q1, c1, v[e]);
+        float t2 = fin ? __builtin_fmaf(r, i2, VX_XQ_MAGIC) : VX_XQ_MAGIC;
+        t2 = fminf(fmaxf(t2, VX_XQ_MAGIC - 127.0f), VX_XQ_MAGIC + 127.0f);
+        // the low byte of MAGIC + n is n mod 256: the int8 of n
+        w1 |= (__float_as_uint(t1) & 0xFFu) << (8 * e);
+        w2 |= (__float_as_uint(t2) & 0xFFu) << (8 * e);
+    }
+    if (in) {
+        // position dword dw (positions 4 dw..4 dw + 3, elements 4t..4t+3) of
+        // level L sits at ((item B + b) 2 + L) 256 + (dw / 2) 64 + (j % 8) 8 + (dw % 2) 4
+        const uint32_t dw = t < 4u ? 2u * t : 2u * (t - 4u) + 1u;
+        uint8_t* base = (uint8_t*)a.levels + ((uint64_t)(j >> 3) * a.B + b) * 512u + (dw >> 1) * 64u + (j & 7u) * 8u +
+                        (dw & 1u) * 4u;
+        *(uint32_t*)base = w1;
+        *(uint32_t*)(base + 256u) = w2;
+        if (t == 0) *(float2*)(a.scales + 2u * grp) = float2{fin ? c2 : m + S, S};
     }
 }

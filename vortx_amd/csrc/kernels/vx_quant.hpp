@@ -32,24 +32,10 @@ __device__ __forceinline__ float vx_f16_to_f32(uint32_t bits) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xFFFFu));
 }
 
-// Weight loads. VX_WEIGHT_NT selects the non-temporal (streaming) hint.
-#ifndef VX_WEIGHT_NT
-#define VX_WEIGHT_NT 0
-#endif
-__device__ __forceinline__ u32x4_a4 vx_ld16(const uint8_t* p) {
-#if VX_WEIGHT_NT
-    return __builtin_nontemporal_load((const u32x4_a4*)p);
-#else
-    return *(const u32x4_a4*)p;
-#endif
-}
-__device__ __forceinline__ uint32_t vx_ld4(const uint8_t* p) {
-#if VX_WEIGHT_NT
-    return __builtin_nontemporal_load((const uint32_t*)p);
-#else
-    return *(const uint32_t*)p;
-#endif
-}
+// Weight loads (plain cached loads: a non-temporal hint measured slower,
+// the x loads then arrive later).
+__device__ __forceinline__ u32x4_a4 vx_ld16(const uint8_t* p) { return *(const u32x4_a4*)p; }
+__device__ __forceinline__ uint32_t vx_ld4(const uint8_t* p) { return *(const uint32_t*)p; }
 
 // v_and_b32 / v_xor_b32 the optimiser cannot see through: applied to a
 // whole dword before byte extraction, they keep each byte->float convert a

@@ -79,6 +79,10 @@ struct vx_context {
     size_t lds_per_block = 65536;
     hipModule_t mods[vx::kNumModules] = {};
     hipFunction_t fn[vx::K_COUNT] = {};
+    // activation workspace of vx_gemv_q at B >= 2 (grown on demand)
+    std::mutex ws_mu;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
 };
 
 namespace vx {
@@ -287,8 +291,11 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
     float alpha = 1.f, beta = 0.f;
     bool broadcast = false;
     if (opts) {
-        if (opts->reserved != 0 || (opts->flags & ~(uint32_t)VX_GEMM_BROADCAST))
+        if (opts->reserved != 0 ||
+            (opts->flags & ~(uint32_t)(VX_GEMM_BROADCAST | VX_GEMM_TILE_NARROW | VX_GEMM_TILE_WIDE)))
             return fail(VX_ERR_INVALID, "unknown gemm option flags (reserved must be 0)");
+        if ((opts->flags & VX_GEMM_TILE_NARROW) && (opts->flags & VX_GEMM_TILE_WIDE))
+            return fail(VX_ERR_INVALID, "VX_GEMM_TILE_NARROW and VX_GEMM_TILE_WIDE are exclusive");
         alpha = opts->alpha;
         beta = opts->beta;
         broadcast = (opts->flags & VX_GEMM_BROADCAST) != 0;
@@ -354,7 +361,8 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
     // 128 x 256 tiles (two workgroups per CU) instead of 128 x 128 (three per
     // CU) when they fill the last round of resident workgroups clearly
     // better: 4096^3 is 1024 narrow tiles, 1.33 rounds of 768, but 512 wide
-    // ones, one round of 512. VX_GEMM_WIDE=0 / 1 forces the choice.
+    // ones, one round of 512. VX_GEMM_TILE_NARROW / _WIDE (vx_gemm_f32_ex)
+    // force the choice; both give the same bits.
     bool wide = false;
     if (am == 0 && (bm == 0 || bm == 1)) {
         const uint64_t tn = (uint64_t)a.tiles_m * a.tiles_n * batch;
@@ -363,9 +371,8 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
         const double en = (double)tn / (double)(((tn + sn - 1) / sn) * sn);
         const double ew = (double)tw / (double)(((tw + sw - 1) / sw) * sw);
         wide = ew > en + 0.05;
-        const char* wenv = std::getenv("VX_GEMM_WIDE");
-        if (wenv && wenv[0] == '0') wide = false;
-        if (wenv && wenv[0] == '1') wide = true;
+        if (opts && (opts->flags & VX_GEMM_TILE_NARROW)) wide = false;
+        if (opts && (opts->flags & VX_GEMM_TILE_WIDE)) wide = true;
     }
     if (wide) {
         a.tiles_n = (p.N + 255) / 256;
@@ -433,19 +440,18 @@ static int bn_kernel(uint32_t qt, int NB) {
     return tab[q_index(qt)][ni];
 }
 
-static int p1_kernel(uint32_t qt, int wgt) {
-    static const int tab[3][2] = {{K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q4_0_w512},
-                                  {K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q8_0_w512},
-                                  {K_vx_gemv_p1_q4_k_w1024, K_vx_gemv_p1_q4_k_w512}};
-    return tab[q_index(qt)][wgt == 1024 ? 0 : 1];
+// Persistent batch-1 kernel with f32 x (VX_GEMV_X_F32).
+static int p1_kernel(uint32_t qt) {
+    static const int tab[3] = {K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q4_k_w1024};
+    return tab[q_index(qt)];
 }
 
-// Persistent batch-1 kernel on the integer-dot path, by ring depth P.
+// Persistent batch-1 kernel on the integer-dot path, by ring depth P (1 or 2).
 static int p1i_kernel(uint32_t qt, int P) {
     switch (q_index(qt)) {
-    case 0: return P >= 3 ? K_vx_gemv_p1i_q4_0_p3 : K_vx_gemv_p1i_q4_0_p2;
+    case 0: return K_vx_gemv_p1i_q4_0_p2;
     case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
-    default: return P >= 3 ? K_vx_gemv_p1i_q4_k_p3 : K_vx_gemv_p1i_q4_k_p2;
+    default: return K_vx_gemv_p1i_q4_k_p2;
     }
 }
 
@@ -474,16 +480,202 @@ static int dequant_kernel(uint32_t qt) {
 }
 
 // Rows per wave for batch 1: the largest R whose grid still gives every
-// CU at least two workgroups (VX_GEMV_R overrides, for tuning sweeps).
+// CU at least two workgroups.
 static int pick_rows_per_wave(vx_ctx ctx, uint32_t qt, uint32_t M) {
-    if (const char* e = std::getenv("VX_GEMV_R")) {
-        const int r = std::atoi(e);
-        if (r == 1 || r == 2 || r == 4 || r == 8) return r;
-    }
     const int maxr = qt == VX_Q8_0 ? 4 : 8;
     for (int r = maxr; r > 1; r >>= 1)
         if ((M + 4u * r - 1) / (4u * r) >= 2u * (uint32_t)ctx->num_cus) return r;
     return 1;
+}
+
+// ------------------------------------------------- activation split
+// vx_xq layout: levels [ceil(K/256) items][B][2][4][8][8] bytes, then scales
+// f32 [K/32][B][2]
+static uint64_t xq_levels_bytes(uint32_t K, uint32_t B) { return (uint64_t)((K + 255u) / 256u) * B * 512u; }
+
+static int xq_size(uint32_t K, uint32_t B, uint64_t* bytes) {
+    if (K % 32u) return fail(VX_ERR_UNSUPPORTED, "activation split: K is not a multiple of 32");
+    *bytes = xq_levels_bytes(K, B) + (uint64_t)(K / 32u) * B * 8u;
+    return VX_OK;
+}
+
+static int check_xq(const vx_xq* q) {
+    if (!q) return fail(VX_ERR_INVALID, "null vx_xq");
+    uint64_t nb;
+    int s = xq_size(q->K, q->B, &nb);
+    if (s) return s;
+    if (nb && !q->base) return fail(VX_ERR_INVALID, "null vx_xq base");
+    if (((uintptr_t)q->base & 15u) != 0) return fail(VX_ERR_INVALID, "vx_xq base is not 16-byte aligned");
+    return VX_OK;
+}
+
+// x [K, B] view -> split into q (already checked). x is canonical [.., K, B].
+static int launch_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* q, const Canon& cx) {
+    const uint32_t K = q->K, B = q->B;
+    vx_xq_args a{};
+    a.x = (const float*)cx.ptr;
+    a.xs_k = cx.l.stride[2];
+    a.xs_b = cx.l.stride[3];
+    a.levels = (int8_t*)q->base;
+    a.scales = (float*)((uint8_t*)q->base + xq_levels_bytes(K, B));
+    a.K = K;
+    a.B = B;
+    a.nblk = K / 32u;
+    a.x_vec = (a.xs_k == 1 && aligned16(cx.ptr) && (B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
+    const uint64_t threads = (uint64_t)a.nblk * B * 8u;
+    if ((threads + 255u) / 256u > 0x7FFFFFFFull) return fail(VX_ERR_UNSUPPORTED, "activation split too large");
+    return launch(ctx, K_vx_quantize_x, dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, stream, a);
+}
+
+// canonical [.., K, B] view of a rank-1 or rank-2 x
+static int canon_x(const vx_cview* x, Canon* cx) {
+    if (!x) return fail(VX_ERR_INVALID, "null view");
+    if (x->layout.rank < 1 || x->layout.rank > 2) return fail(VX_ERR_SHAPE, "x must be [K] or [K, B]");
+    vx_layout lx = x->layout;
+    int s;
+    if (lx.rank == 1 && (s = layout_unsqueeze(&x->layout, 1, &lx))) return s;
+    return canon_view(x->base, &lx, cx, "x");
+}
+
+static int run_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* q, const vx_cview* x) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    int s = check_xq(q);
+    if (s) return s;
+    Canon cx;
+    if ((s = canon_x(x, &cx))) return s;
+    if (cx.l.size[2] != q->K || cx.l.size[3] != q->B) {
+        static thread_local std::string m;
+        m = "activation split: x " + layout_str(cx.l) + " is not [K=" + std::to_string(q->K) + ", B=" +
+            std::to_string(q->B) + "]";
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    if (q->K == 0 || q->B == 0) return VX_OK;
+    DeviceGuard guard(ctx->device);
+    return launch_quantize_x(ctx, stream, q, cx);
+}
+
+// Batched GEMV kernel on split x: column groups ncg (1: B <= 8, 2: B <= 16),
+// items per wave and pass xi, one pass or several (mp; K past 16 xi items).
+// The multi-pass kernels use the largest xi of their format.
+static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp) {
+    switch (q_index(qt)) {
+    case 0:
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_0_c2_x1_mp : K_vx_gemv_xq_q4_0_c2_x1;
+        if (mp) return K_vx_gemv_xq_q4_0_c1_x3_mp;
+        return xi == 1 ? K_vx_gemv_xq_q4_0_c1_x1 : xi == 2 ? K_vx_gemv_xq_q4_0_c1_x2 : K_vx_gemv_xq_q4_0_c1_x3;
+    case 1:
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q8_0_c2_x1_mp : K_vx_gemv_xq_q8_0_c2_x1;
+        if (mp) return K_vx_gemv_xq_q8_0_c1_x2_mp;
+        return xi == 1 ? K_vx_gemv_xq_q8_0_c1_x1 : K_vx_gemv_xq_q8_0_c1_x2;
+    default:
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_k_c2_x1_mp : K_vx_gemv_xq_q4_k_c2_x1;
+        if (mp) return K_vx_gemv_xq_q4_k_c1_x2_mp;
+        return xi == 1 ? K_vx_gemv_xq_q4_k_c1_x1 : K_vx_gemv_xq_q4_k_c1_x2;
+    }
+}
+
+// y [.., M, B] (canonical) = W x, x given by its split q (q->K == K, q->B == B).
+// Launches of up to 16 columns; W is streamed once per launch.
+static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const vx_qweight* w, const vx_xq* q) {
+    const uint32_t M = w->rows, K = w->cols, B = q->B;
+    vx_gemv_xq_args a{};
+    a.w = (const uint8_t*)w->base;
+    a.row_stride = w->row_stride_bytes;
+    a.levels = (const int8_t*)q->base;
+    a.scales = (const float*)((const uint8_t*)q->base + xq_levels_bytes(K, B));
+    a.ys_m = cy.l.stride[2];
+    a.ys_b = cy.l.stride[3];
+    a.M = M;
+    a.K = K;
+    a.nblk = K / 32u;
+    a.nunits = K / 64u;
+    a.ipr = (a.nunits + 3u) / 4u;
+    a.xcols = B;
+    // items per wave and pass: x levels of XI items stay in registers (Q8_0's
+    // larger weight items leave room for two, Q4_K's header for two)
+    const int ximax = w->qtype == VX_Q4_0 ? 3 : 2;
+    for (uint32_t b0 = 0; b0 < B; b0 += 16u) {
+        a.B = B - b0 < 16u ? B - b0 : 16u;
+        a.col0 = b0;
+        a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
+        const int ncg = a.B > 8u ? 2 : 1;
+        const int xmax = ncg == 2 ? 1 : ximax;
+        int xi = (int)((a.ipr + 15u) / 16u);
+        const bool mp = xi > xmax;
+        if (mp) xi = xmax;
+        a.npass = (a.ipr + 16u * (uint32_t)xi - 1u) / (16u * (uint32_t)xi);
+        // 64 KB of parked partial sums + each of the 16 waves' scales
+        const size_t lds = 65536u + (size_t)16u * 8u * (uint32_t)xi * 8u * (uint32_t)ncg * 8u;
+        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream,
+                       a);
+        if (s) return s;
+    }
+    return VX_OK;
+}
+
+static bool xq_layout_ok(const vx_qweight* w) {
+    return w->cols > 0 && w->cols % 64u == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
+}
+
+// canonical [.., M, B] view of a rank-1 or rank-2 y
+static int canon_y(const vx_mview* y, Canon* cy) {
+    if (!y) return fail(VX_ERR_INVALID, "null view");
+    if (y->layout.rank < 1 || y->layout.rank > 2) return fail(VX_ERR_SHAPE, "y must be [M] or [M, B]");
+    vx_layout ly = y->layout;
+    int s;
+    if (ly.rank == 1 && (s = layout_unsqueeze(&y->layout, 1, &ly))) return s;
+    return canon_view(y->base, &ly, cy, "y");
+}
+
+static int run_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_xq* q) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    uint32_t qk, bb;
+    int s = check_qweight(w, &qk, &bb);
+    if (s) return s;
+    if ((s = check_xq(q))) return s;
+    Canon cy;
+    if ((s = canon_y(y, &cy))) return s;
+    if (cy.l.size[2] != w->rows || q->K != w->cols || cy.l.size[3] != q->B) {
+        static thread_local std::string m;
+        m = "incompatible gemv shapes: y " + layout_str(cy.l) + " = W [" + std::to_string(w->rows) + ", " +
+            std::to_string(w->cols) + "] x split [K=" + std::to_string(q->K) + ", B=" + std::to_string(q->B) + "]";
+        return fail(VX_ERR_SHAPE, m.c_str());
+    }
+    if (w->rows == 0 || q->B == 0) return VX_OK;
+    if (!xq_layout_ok(w))
+        return fail(VX_ERR_UNSUPPORTED, "vx_gemv_q_xq needs K a multiple of 64 and 4-byte aligned weight rows");
+    DeviceGuard guard(ctx->device);
+    return launch_gemv_xq(ctx, stream, cy, w, q);
+}
+
+// The context's activation workspace, at least `bytes` large.
+static int workspace(vx_ctx ctx, vx_stream stream, size_t bytes, void** out) {
+    std::lock_guard<std::mutex> lock(ctx->ws_mu);
+    if (ctx->ws_bytes < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return fail(VX_ERR_UNSUPPORTED,
+                        "vx_gemv_q: the activation workspace must grow, which cannot happen during stream capture "
+                        "(make one call of this size before capturing)");
+        if (ctx->ws) {
+            hipError_t e = hipDeviceSynchronize();  // the old buffer may still be in use
+            if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
+            (void)hipFree(ctx->ws);
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        const size_t sz = (bytes + (1u << 20) - 1u) & ~(size_t)((1u << 20) - 1u);  // whole MiB
+        hipError_t e = hipMalloc(&ctx->ws, sz);
+        if (e != hipSuccess) {
+            ctx->ws = nullptr;
+            return fail_hip(e, "hipMalloc (activation workspace)");
+        }
+        ctx->ws_bytes = sz;
+    }
+    *out = ctx->ws;
+    return VX_OK;
 }
 
 static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
@@ -527,11 +719,21 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
 
     const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
-    // x as two int8 levels per 32-block (the default) or exact f32
-    // (VX_GEMV_X_F32, or VX_GEMV_BATCHED=simt for batches only)
+    // x as two int8 levels per 32-block (the default) or exact f32 (VX_GEMV_X_F32)
     const bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
-    const char* bmode = std::getenv("VX_GEMV_BATCHED");
-    const bool force_simt = x_f32 || (bmode && std::strcmp(bmode, "simt") == 0);
+    const bool force_simt = x_f32;
+    if (B >= 2 && !force_simt && xq_layout_ok(w)) {
+        // split x once into the context's workspace, then the matrix-core
+        // GEMV on the split (W streamed once per 16 columns)
+        vx_xq q{nullptr, K, B};
+        uint64_t nb;
+        if ((s = xq_size(K, B, &nb))) return s;
+        if ((s = workspace(ctx, stream, (size_t)nb, &q.base))) {
+            return s;
+        }
+        if ((s = launch_quantize_x(ctx, stream, &q, cx))) return s;
+        return launch_gemv_xq(ctx, stream, cy, w, &q);
+    }
     if (B >= 2 && fast && !force_simt) {
         // int8 matrix-core path, one workgroup per CU, up to 8 columns per
         // launch (fewer when x of that many columns does not fit LDS).
@@ -554,11 +756,9 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             return VX_OK;
         }
     }
-    // batch-1 kernel: the persistent one (default), or the per-row-group
-    // one with VX_GEMV_B1=rows (also used when x does not fit its LDS:
-    // K > 16384); int8 x unless VX_GEMV_X_F32
-    const char* b1env = std::getenv("VX_GEMV_B1");
-    const bool b1_rows = b1env && std::strcmp(b1env, "rows") == 0;
+    // batch-1 kernel: the persistent one, or the per-row-group one when x
+    // does not fit the persistent kernel's LDS (K > 16384); int8 x unless
+    // VX_GEMV_X_F32
     uint32_t b0 = 0;
     while (b0 < B) {
         const uint32_t rem = B - b0;
@@ -574,7 +774,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         int k;
         uint32_t rows_per_wg;
         size_t lds;
-        if (NB == 1 && !x_f32 && a.nunits <= 256u && !b1_rows) {
+        if (NB == 1 && !x_f32 && a.nunits <= 256u) {
             // persistent integer-dot path: all of x as int8 levels, 152 B per unit
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
@@ -601,15 +801,13 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             k = i8b1_kernel(w->qtype, R);
             rows_per_wg = 4u * R;
             lds = (size_t)a.upitch * 152u;
-        } else if (NB == 1 && a.nunits <= 256u && !b1_rows) {
+        } else if (NB == 1 && a.nunits <= 256u) {
             // Persistent path: one workgroup per CU, all of x in LDS
             // (16 slots x odd pitch x 16 B) plus the per-unit block sums.
-            int wgt = 1024;
-            if (const char* e = std::getenv("VX_P1_WG")) wgt = std::atoi(e) == 512 ? 512 : 1024;
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
             lds = (size_t)16u * a.upitch * 16u + (size_t)a.nunits * 8u;
-            s = launch(ctx, p1_kernel(w->qtype, wgt), dim3((uint32_t)ctx->num_cus), dim3((uint32_t)wgt), lds, stream, a);
+            s = launch(ctx, p1_kernel(w->qtype), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
@@ -821,6 +1019,10 @@ int vx_destroy(vx_ctx ctx) {
     vx::clear_error();
     if (!ctx) return VX_OK;
     vx::DeviceGuard guard(ctx->device);
+    if (ctx->ws) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->ws);
+    }
     for (hipModule_t m : ctx->mods)
         if (m) (void)hipModuleUnload(m);
     delete ctx;
@@ -871,6 +1073,20 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
     if ((flags & VX_GEMV_X_INT8) && (flags & VX_GEMV_X_F32))
         return vx::fail(VX_ERR_INVALID, "VX_GEMV_X_INT8 and VX_GEMV_X_F32 are exclusive");
     return vx::run_gemv_q(ctx, stream, y, w, x, flags);
+}
+
+int vx_xq_size(uint32_t K, uint32_t B, uint64_t* bytes) {
+    vx::clear_error();
+    if (!bytes) return vx::fail(VX_ERR_INVALID, "null bytes");
+    return vx::xq_size(K, B, bytes);
+}
+
+int vx_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* out, const vx_cview* x) {
+    return vx::run_quantize_x(ctx, stream, out, x);
+}
+
+int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_xq* x) {
+    return vx::run_gemv_q_xq(ctx, stream, y, w, x);
 }
 
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {

@@ -89,4 +89,34 @@ typedef struct vx_quant_args {
     uint32_t x_vec;  /* 1: xs_k == 1 and 16-byte aligned rows */
 } vx_quant_args;
 
+/* Activation split x [K, B] f32 -> levels int8 [nblk][B][2][32] and scales
+ * f32 [nblk][B][2] (the layout of vx_xq in include/vortx_hip.h). */
+typedef struct vx_xq_args {
+    const float* x;        /* x[k, b] at x[k*xs_k + b*xs_b] */
+    int64_t xs_k, xs_b;
+    int8_t* levels;
+    float* scales;
+    uint32_t K, B;
+    uint32_t nblk;         /* K / 32 */
+    uint32_t x_vec;        /* 1: xs_k == 1, 16-byte aligned columns */
+} vx_xq_args;
+
+/* Batched GEMV on split activations: y[m, b] = sum_k W[m, k] x[k, b]. */
+typedef struct vx_gemv_xq_args {
+    const uint8_t* w;
+    uint64_t row_stride;   /* bytes between rows of W */
+    const int8_t* levels;  /* the vx_xq levels of x */
+    const float* scales;   /* the vx_xq scales of x */
+    float* y;              /* y[m, b] at y[m*ys_m + b*ys_b] */
+    int64_t ys_m, ys_b;
+    uint32_t M, K, B;      /* B: columns of this launch, <= 16 */
+    uint32_t nblk;         /* K / 32 */
+    uint32_t nunits;       /* K / 64 */
+    uint32_t ipr;          /* items (256 weights) per row, the last one possibly partial */
+    uint32_t npass;        /* passes over K: ceil(ipr / (16 * items per wave)) */
+    uint32_t xcols;        /* columns of the split x (its layout pitch) */
+    uint32_t col0;         /* first split-x column of this launch (y is already offset) */
+    uint32_t pad0;
+} vx_gemv_xq_args;
+
 #endif /* VX_KARGS_H */
