@@ -211,7 +211,7 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
  * one context must therefore not overlap in time on different streams, and
  * the first call of a given size must not be made during stream capture
  * (VX_ERR_UNSUPPORTED then). Callers that cannot allocate use
- * vx_quantize_x + vx_gemv_q_xq on buffers of their own. */
+ * vx_gemv_q_noalloc or vx_quantize_x + vx_gemv_q_xq on buffers of their own. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 
@@ -274,6 +274,23 @@ int vx_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* out, const vx_cview
  * nothing here. */
 int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_xq* x);
+
+/* vx_gemv_q_ex that allocates nothing. No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, flags, kernels and results as vx_gemv_q_ex; where that one
+ * splits x into the context's workspace (B >= 2), this one uses a fixed
+ * device array of VX_NOALLOC_SCRATCH_BYTES (4 MiB) that the library's GEMV
+ * code object holds per context from vx_init to vx_destroy, so the split of
+ * x, vx_xq_size(K, B) bytes (72 per 32 elements of x), must fit it (else
+ * VX_ERR_UNSUPPORTED, nothing launched): B = 16 up to K = 116480, B = 64 up
+ * to K = 28928. Every call on
+ * one context uses the same array: calls that overlap in time on one
+ * context race (serialize them on one stream, or use one context per
+ * stream); nothing in it needs to start at zero. */
+#define VX_NOALLOC_SCRATCH_BYTES (4u << 20)
+int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y,
+                      const vx_qweight* w, const vx_cview* x, uint32_t flags);
 
 /* out[m, k] = W[m, k] decoded to f32 (bit-exact: every block value is
  * exactly representable in f32). out is an [M, K] view, any strides. */

@@ -81,6 +81,7 @@ SIGNATURES = [
     ("vx_xq_size", C.c_int, [C.c_uint32, C.c_uint32, _P(C.c_uint64)]),
     ("vx_quantize_x", C.c_int, [C.c_void_p, C.c_void_p, _P(VxXq), _P(VxCView)]),
     ("vx_gemv_q_xq", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxXq)]),
+    ("vx_gemv_q_noalloc", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight), _P(VxCView), C.c_uint32]),
     ("vx_quantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxQWeight), _P(VxCView)]),
     ("vx_contiguous", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxCView), C.c_void_p]),
     ("vx_qtype_info", C.c_int, [C.c_uint32, _P(C.c_uint32), _P(C.c_uint32)]),

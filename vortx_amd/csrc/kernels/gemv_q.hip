@@ -1401,6 +1401,16 @@ __device__ __forceinline__ void vx_xq_prepare(uint32_t (&r)[vx_unit<QT>::NW], ui
 #define VX_XQ_WG 1024
 typedef long i64x2 __attribute__((ext_vector_type(2)));
 
+// Scratch of vx_gemv_q_noalloc (no counterpart in the reference): the
+// activation split of x for callers that cannot allocate device memory.
+// One copy per loaded module, i.e. per context; vx_init resolves its device
+// address once (hipModuleGetGlobal, with the context's device current) and
+// the host passes that address to vx_quantize_x / vx_gemv_xq like any other
+// buffer. Calls on one context share it, so calls that overlap in time race.
+extern "C" {
+__device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
+}
+
 // LDS of vx_gemv_xq: per wave, the scales of its K slice in the current
 // pass [8 XI blocks][CP columns] float2 {c2, S'} (S' = -8 S for Q4_0); then
 // red[RMAX tiles][16 slots][CP][16 rows] partial sums.

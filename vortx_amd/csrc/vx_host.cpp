@@ -70,6 +70,7 @@ static const char* const kKernelNames[K_COUNT] = {
 // The embedded code objects; every kernel name is unique across them.
 static const unsigned char* const kModules[] = {vx_co_gemm, vx_co_gemv_q, vx_co_copy, vx_co_quantize};
 constexpr int kNumModules = 4;
+constexpr int kModGemv = 1;  // the module holding vx_scratch
 
 }  // namespace vx
 
@@ -79,6 +80,9 @@ struct vx_context {
     size_t lds_per_block = 65536;
     hipModule_t mods[vx::kNumModules] = {};
     hipFunction_t fn[vx::K_COUNT] = {};
+    // device address of vx_scratch in this context's GEMV module (vx_gemv_q_noalloc)
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
     // activation workspace of vx_gemv_q at B >= 2 (grown on demand)
     std::mutex ws_mu;
     void* ws = nullptr;
@@ -175,6 +179,24 @@ static int init(int device, vx_ctx* out) {
             t_msg = std::string("hipModuleGetFunction(") + kKernelNames[k] + "): " + hipGetErrorString(e);
             return VX_ERR_NO_CODE_OBJECT;
         }
+    }
+    // The no-alloc entry point's scratch: a __device__ array of the GEMV code
+    // object; its address on this device (current here) is resolved once.
+    {
+        hipDeviceptr_t p = nullptr;
+        size_t bytes = 0;
+        e = hipModuleGetGlobal(&p, &bytes, ctx->mods[kModGemv], "vx_scratch");
+        if (e != hipSuccess || !p || bytes != VX_SCRATCH_BYTES) {
+            if (e == hipSuccess) e = hipErrorNotFound;
+            (void)hipGetLastError();
+            unload();
+            delete ctx;
+            t_hip = e;
+            t_msg = std::string("hipModuleGetGlobal(vx_scratch): ") + hipGetErrorString(e);
+            return VX_ERR_NO_CODE_OBJECT;
+        }
+        ctx->scratch = (void*)p;
+        ctx->scratch_bytes = bytes;
     }
     *out = ctx;
     return VX_OK;
@@ -658,7 +680,7 @@ static int workspace(vx_ctx ctx, vx_stream stream, size_t bytes, void** out) {
         if (hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
             return fail(VX_ERR_UNSUPPORTED,
                         "vx_gemv_q: the activation workspace must grow, which cannot happen during stream capture "
-                        "(make one call of this size before capturing)");
+                        "(make one call of this size before capturing, or use vx_gemv_q_noalloc)");
         if (ctx->ws) {
             hipError_t e = hipDeviceSynchronize();  // the old buffer may still be in use
             if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
@@ -679,7 +701,7 @@ static int workspace(vx_ctx ctx, vx_stream stream, size_t bytes, void** out) {
 }
 
 static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
-                      uint32_t flags) {
+                      uint32_t flags, bool noalloc = false) {
     clear_error();
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
     uint32_t qk, bb;
@@ -728,7 +750,17 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         vx_xq q{nullptr, K, B};
         uint64_t nb;
         if ((s = xq_size(K, B, &nb))) return s;
-        if ((s = workspace(ctx, stream, (size_t)nb, &q.base))) {
+        if (noalloc) {
+            // the module's scratch array: no allocation, a fixed maximum
+            if (nb > ctx->scratch_bytes) {
+                static thread_local std::string m;
+                m = "vx_gemv_q_noalloc: the split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) +
+                    "] needs " + std::to_string(nb) + " bytes, more than the " + std::to_string(ctx->scratch_bytes) +
+                    "-byte scratch (ceil(K/256) * B * 512 + (K/32) * B * 8 must not exceed it)";
+                return fail(VX_ERR_UNSUPPORTED, m.c_str());
+            }
+            q.base = ctx->scratch;
+        } else if ((s = workspace(ctx, stream, (size_t)nb, &q.base))) {
             return s;
         }
         if ((s = launch_quantize_x(ctx, stream, &q, cx))) return s;
@@ -1091,6 +1123,15 @@ int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
 
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     return vx::run_dequant(ctx, stream, out, w);
+}
+
+int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
+                      uint32_t flags) {
+    if (flags & ~(uint32_t)(VX_GEMV_X_INT8 | VX_GEMV_X_F32))
+        return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_noalloc flags");
+    if ((flags & VX_GEMV_X_INT8) && (flags & VX_GEMV_X_F32))
+        return vx::fail(VX_ERR_INVALID, "VX_GEMV_X_INT8 and VX_GEMV_X_F32 are exclusive");
+    return vx::run_gemv_q(ctx, stream, y, w, x, flags, true);
 }
 
 int vx_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, const vx_cview* x) {

@@ -119,4 +119,8 @@ typedef struct vx_gemv_xq_args {
     uint32_t pad0;
 } vx_gemv_xq_args;
 
+/* Bytes of the device scratch array of vx_gemv_q_noalloc (vx_scratch in
+ * the GEMV code object): the largest activation split it can hold. */
+#define VX_SCRATCH_BYTES (4u << 20)
+
 #endif /* VX_KARGS_H */
