@@ -8,15 +8,18 @@ cannot serve them), inputs resident in HBM before timing starts.
 
 Secondary lines in the same JSON object: the other BASELINE GEMV configs
 (Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 and 14336 x 4096 b=1,
-Q4_0 4096 x 11008 b=1, Q4_0 11008 x 4096 b=4 and b=8, Q4_K 14336 x 4096
-b=16; GB/s of algorithmic bytes), the contiguous copy of a transposed
+Q4_0 4096 x 11008 b=1, b=4 and b=8, Q4_0 11008 x 4096 b=4 and b=8, Q4_K
+14336 x 4096 and 32000 x 4096 b=16; GB/s of algorithmic bytes), the f32
+GEMV 11008 x 4096 and the same kernel as a read-only stream at the
+headline's size and at 537 MB, the contiguous copy of a transposed
 8192^2 view and a plain streaming copy of a contiguous one (the achievable
 bandwidth beside the 8 TB/s peak), the same streaming copy at the headline's
 size (25.4 MB per launch, graph-replayed: the achievable rate of one launch
 that small), the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
 -> HBM upload (against the PCIe 5.0 x16 link) and the f32 GEMMs 4096^3,
 4096 x 11008 x 4096, 4096^3 with a transposed-B view and the broadcast
-batch (TFLOP/s), each with its roofline, plus CPU baselines from the
+batch (TFLOP/s), and the reference's GEMM size sweep (64..4096, tiled and
+naive), each with its roofline, plus CPU baselines from the
 oracle's OpenMP restatements on the host cores.
 
 Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
@@ -130,6 +133,91 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
         "alg_bytes": alg,
         "weight_copies": ncopy,
     }
+
+
+def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
+    """f32 GEMV y = A x (the GEMM op's N == 1 route, vx_gemv_f32): A [M, K]
+    row-major f32 read once, so 4 M K + 4 K + 4 M algorithmic bytes per launch;
+    A rotating over >= 512 MB of copies, K launches captured into a HIP graph
+    and replayed as in time_gemv. A read-only HBM stream with one FMA per
+    element: the achievable read rate of a launch that size."""
+    import torch
+
+    import vortx_amd as vx
+
+    dev = torch.device("cuda:0")
+    nbytes = 4 * M * K
+    ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
+    log(f"[copies] {ncopy} x {nbytes}")
+    base = [torch.randn((M, K), device=dev) for _ in range(min(4, ncopy))]
+    As = [base[i % len(base)].clone() if i >= len(base) else base[i] for i in range(ncopy)]
+    x = torch.randn((K, 1), device=dev)
+    y = torch.empty((M, 1), device=dev)
+    gm = vx.Gemm(0)
+    for i in range(warmup):
+        gm.dispatch(y, As[i % ncopy], x)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    chunk = min(steps, 500)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(chunk):
+                gm.dispatch(y, As[i % ncopy], x, stream=s)
+    torch.cuda.synchronize()
+    reps = max(1, steps // chunk)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    done = reps * chunk
+    alg = 4 * M * K + 4 * K + 4 * M
+    return {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
+            "avg_launch_ms": e0.elapsed_time(e1) / done, "alg_bytes": alg, "copies": ncopy}
+
+
+def time_gemm_sweep(dims=(64, 128, 256, 512, 768, 1024, 1536, 2048, 4096)):
+    """The reference's GEMM benchmark (examples/gemm_bench.rs): square f32
+    GEMMs of each size, 3 warmup + 10 timed launches of the default (tiled)
+    route and of the naive kernel, average launch time from HIP events."""
+    import torch
+
+    import vortx_amd as vx
+    from vortx_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    gm = vx.Gemm(0)
+    pts = []
+    for d in dims:
+        a = S.uniform((d, d), 1, dev)
+        b = S.uniform((d, d), 2, dev)
+        c = torch.empty((d, d), device=dev)
+        row = {"dim": d}
+        for name, fn in (("tiled", gm.dispatch), ("naive", gm.dispatch_naive)):
+            for _ in range(3):
+                fn(c, a, b)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                fn(c, a, b)
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 10
+            row[f"{name}_ms"] = ms
+            row[f"{name}_tflops"] = 2.0 * d ** 3 / (ms * 1e-3) / 1e12
+        row["speedup"] = row["naive_ms"] / row["tiled_ms"]
+        pts.append(row)
+        log(f"[gemm_sweep] {row}")
+    return pts
 
 
 def time_gemm(M: int, N: int, K: int, steps: int, warmup: int, transb: bool = False):
@@ -451,6 +539,15 @@ def main() -> int:
         r = time_gemv(qt, M, K, B, steps, args.warmup, label)
         log(f"[{label}] {r}")
         sec.append((workload, prof, r))
+    gv32 = time_gemv_f32(11008, 4096, max(100, args.steps // 4), args.warmup)
+    log(f"[gemv_f32] {gv32}")
+    # read-only streams through the same kernel: the headline's size (1552 x
+    # 4096 f32 = 25.43 MB, the Q4_0 GEMV moves 25.42 MB) and >= 512 MB
+    ro25 = time_gemv_f32(1552, 4096, args.steps, args.warmup)
+    log(f"[read_25mb] {ro25}")
+    ro512 = time_gemv_f32(32768, 4096, max(50, args.steps // 20), max(5, args.warmup // 20))
+    log(f"[read_512mb] {ro512}")
+    sweep = time_gemm_sweep()
     gsteps = max(5, min(50, args.steps // 40))
     gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
     log(f"[gemm] {gemm}")
@@ -519,6 +616,18 @@ def main() -> int:
             {"workload": wl, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
              "dtype": DT_INT8X, "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
         ] + [
+            {"workload": "f32 GEMV y = A x, A 11008x4096 row-major (the GEMM op's N == 1 route, vx_gemv_f32), "
+                         "A rotating over >= 512 MB, HIP-graph replay", "value": gv32["value"], "unit": "GB/s",
+             "ms_per_step": gv32["ms_per_step"], "dtype": "f32", "roofline": roof_hbm(gv32, "gemv_f32_11008x4096")},
+            {"workload": "read-only HBM stream of the headline's size: vx_gemv_f32 on A 1552x4096 f32 (25.43 MB "
+                         "read per launch; the Q4_0 GEMV reads 25.42 MB), A rotating over >= 512 MB, HIP-graph "
+                         "replay (the achievable read rate of one launch this size)", "value": ro25["value"],
+             "unit": "GB/s", "ms_per_step": ro25["ms_per_step"], "dtype": "f32",
+             "roofline": roof_hbm(ro25, "gemv_f32_1552x4096")},
+            {"workload": "read-only HBM stream, 537 MB per launch: vx_gemv_f32 on A 32768x4096 f32 (the achievable "
+                         "read rate of a long stream)", "value": ro512["value"], "unit": "GB/s",
+             "ms_per_step": ro512["ms_per_step"], "dtype": "f32", "roofline": roof_hbm(ro512, "gemv_f32_32768x4096")},
+        ] + [
             {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
              "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],
              "roofline": roof_hbm(cont, "contiguous_t8192")},
@@ -560,6 +669,9 @@ def main() -> int:
                          "(vx_gemm_f32_ex, beta = 1)", "value": gemm_b["value"], "unit": "TFLOP/s",
              "ms_per_step": gemm_b["ms_per_step"],
              "roofline": roof_mfma(gemm_b, "gemm_f32_broadcast_8x1024")},
+            {"workload": "f32 GEMM sweep of the reference's benchmark (examples/gemm_bench.rs: dim^3 for dim in "
+                         "64..4096, 3 warmup + 10 timed launches each), default tiled route and naive kernel",
+             "unit": "TFLOP/s", "value": sweep[-1]["tiled_tflops"], "points": sweep},
         ],
     }
     print(json.dumps(line), flush=True)

@@ -63,6 +63,8 @@ def lib():
         L.orc_f32_to_f16.restype = C.c_uint16
         L.orc_quantize.argtypes = [C.c_uint32, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_uint64]
         L.orc_quantize.restype = C.c_int
+        L.orc_q4k_fit.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.POINTER(C.c_float), C.POINTER(C.c_float)]
+        L.orc_q4k_fit.restype = C.c_int
         L.orc_quantize_x.argtypes = [C.c_void_p, C.c_int64, C.c_int64, C.c_uint32, C.c_uint32, C.c_void_p,
                                      C.c_void_p]
         L.orc_quantize_x.restype = C.c_int
@@ -237,6 +239,18 @@ def quantize(qtype: int, x: np.ndarray) -> np.ndarray:
     rc = lib().orc_quantize(qtype, _ptr(x), M, K, K, _ptr(out), rb)
     assert rc == 0, rc
     return out
+
+
+def q4k_fit(x: np.ndarray, weights: np.ndarray):
+    """One Q4_K sub-block's scale/min search (ggml make_qkx2_quants with the
+    constants quantize_row_q4_K_ref passes) -> (levels uint8[32], scale, min)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    assert x.shape == w.shape == (32,)
+    levels = np.zeros(32, np.uint8)
+    sc, mn = C.c_float(), C.c_float()
+    assert lib().orc_q4k_fit(_ptr(x), _ptr(w), _ptr(levels), C.byref(sc), C.byref(mn)) == 0
+    return levels, sc.value, mn.value
 
 
 # ---------------------------------------------------- activation split

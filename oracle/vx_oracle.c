@@ -547,6 +547,20 @@ static void orc_quant_q4_0(const float* x, uint8_t* y) {
     }
 }
 
+/* ggml's search constants for Q4_K sub-blocks (quantize_row_q4_K_ref calls
+ * make_qkx2_quants(32, 15, x, weights, L, &min, Laux, -1, 0.1, 20)):
+ * candidate inverse scales (15 + rmin + rdelta k) / (max - min), k = 0..20. */
+#define ORC_Q4K_RMIN (-1.f)
+#define ORC_Q4K_RDELTA 0.1f
+#define ORC_Q4K_NSTEP 20
+
+/* One sub-block's scale search, as orc_quant_q4_k runs it (test hook). */
+int orc_q4k_fit(const float* x, const float* weights, uint8_t* L, float* scale, float* min) {
+    uint8_t Laux[32];
+    *scale = orc_make_qkx2(32, 15, x, weights, L, min, Laux, ORC_Q4K_RMIN, ORC_Q4K_RDELTA, ORC_Q4K_NSTEP);
+    return 0;
+}
+
 static void orc_quant_q4_k(const float* x, uint8_t* y) {
     uint8_t L[256], Laux[32];
     float weights[32], mins[8], scales[8];
@@ -556,7 +570,8 @@ static void orc_quant_q4_k(const float* x, uint8_t* y) {
         for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
         const float av_x = sqrtf(sum_x2 / 32);
         for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-        scales[j] = orc_make_qkx2(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+        scales[j] = orc_make_qkx2(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, ORC_Q4K_RMIN,
+                                  ORC_Q4K_RDELTA, ORC_Q4K_NSTEP);
         if (scales[j] > max_scale) max_scale = scales[j];
         if (mins[j] > max_min) max_min = mins[j];
     }

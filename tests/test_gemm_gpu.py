@@ -225,3 +225,39 @@ def test_gemm_1024_config(gemm):
     gemm.dispatch(c, a, b)
     torch.cuda.synchronize()
     assert_close(c.cpu().numpy(), _f64(a, b)[0, 0])
+
+
+@pytest.mark.parametrize("M,K,pad", [(32, 4, 0), (37, 5, 3), (45, 256, 0), (300, 1000, 4), (129, 4096, 0),
+                                     (61, 4099, 1), (33, 11008, 0), (1000, 16384, 0), (35, 20000, 0)])
+def test_gemv_route_shapes(gemm, M, K, pad):
+    """The N == 1 route (M >= 32; one row per workgroup from K = 4096, four below):
+    ragged M and K (K % 4 != 0 with the rows padded to a multiple of 4),
+    strided x; float64 reference, normwise tolerance."""
+    note(f"f32 gemv {M}x{K} pad {pad}")
+    buf = S.uniform((M, K + pad), 5, DEV)
+    a = buf[:, :K]
+    if (K + pad) % 4:
+        pytest.skip("the route needs rows 16-byte aligned")
+    xb = S.uniform((K, 3), 6, DEV)
+    for x in (xb[:, :1].contiguous(), xb[:, 1:2]):  # contiguous and strided x
+        out = _nan(M, 1)
+        assert vx.Gemm.route(out, a, x) == vx.ROUTE_GEMV
+        gemm.dispatch(out, a, x)
+        torch.cuda.synchronize()
+        ref = _f64(a, x)[0, 0]
+        err = np.abs(out.cpu().numpy() - ref).max() / max(np.abs(ref).max(), 1e-30)
+        assert err <= 1e-5, (M, K, err)
+
+
+def test_gemv_route_batch_and_epilogue(gemm):
+    """Batched A and x with alpha / beta: out = 0.5 A x + 2 out."""
+    note("f32 gemv batch alpha beta")
+    a = S.uniform((3, 700, 4096), 7, DEV)
+    x = S.uniform((3, 4096, 1), 8, DEV)
+    c0 = S.uniform((3, 700, 1), 9, DEV)
+    out = c0.clone()
+    gemm.dispatch_ex(out, a, x, alpha=0.5, beta=2.0)
+    torch.cuda.synchronize()
+    ref = 0.5 * (a.double() @ x.double()) + 2.0 * c0.double()
+    err = ((out.double() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= 1e-5, err

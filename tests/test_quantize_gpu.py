@@ -168,3 +168,20 @@ def test_quantize_output_layouts(qgemv, qtype, layout):
     else:
         f = flat.cpu().numpy()
         assert (f[:2] == 0xAB).all() and (f[2 + M * rb:] == 0xAB).all(), "wrote outside the output"
+
+
+def test_quantize_q4_k_search_fixture(qgemv):
+    """The designed Q4_K sub-blocks of tests/golden/q4k_search.json: the block
+    whose result depends on the av_x + |x| weighting equals the fixture's
+    bytes; a row of the search-winner sub-blocks equals the oracle's bytes."""
+    import json
+    import os
+    fix = json.load(open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "q4k_search.json")))
+    x = np.zeros((2, 256), np.float32)
+    x[0, :32] = np.array(fix["weighting_block"]["x0_bits"], np.uint32).view(np.float32)
+    for i, c in enumerate(fix["fits"]):
+        x[1, 32 * i:32 * i + 32] = np.array(c["x_bits"], np.uint32).view(np.float32)
+    note("quantize q4_k search fixture")
+    got = _run(qgemv, vx.VX_Q4_K, x)
+    assert got[0].tobytes().hex() == fix["weighting_block"]["block_hex"]
+    assert np.array_equal(got[1], O.quantize(vx.VX_Q4_K, x[1:2])[0])

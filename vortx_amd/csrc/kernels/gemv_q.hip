@@ -790,348 +790,7 @@ __device__ __forceinline__ void vx_gemv_bn(const vx_gemv_args& a) {
     }
 }
 
-// ------------------------------------------------------------------------
-// Batched GEMV (2..8 columns per launch) on int8 matrix cores
-// (v_mfma_i32_16x16x64_i8).
-//   Per column and 32-block, x is split into two int8 levels,
-//     x ~= c2 (254 x1 + x2),  c2 = max|x_blk| / (126 * 254),
-//   so |x - that| <= c2 / 2 ~ 1.6e-5 max|x_blk|; the levels are staged in
-//   LDS as [column][unit][level][64 elements] with {c2, S = sum x} per
-//   block. Products and sums over a block are exact in int32.
-//   Rounds as in vx_gemv_p1's row tiles: a wave owns a 16-row tile, and in
-//   round q lane (row j = l%16, o = l/16) holds all of unit 4q + o of row j
-//   (loaded coalesced by lane 4j + o and moved with ds_bpermute).
-//   MFMA (s, cp) covers elements 16s..16s+15 of the four units for the
-//   column pair cp: k-group o of the B operand is lane (j, o)'s own piece s
-//   (exact int8), and A row 4o + 2c + L holds level L of column 2cp + c for
-//   unit 4q + o in k-group o only, so D row 4o + 2c + L lands in lane (j, o)
-//   (register 2c + L): the level sums of the lane's own unit. The lane then
-//   applies its block scales: acc += s_t c2 (254 D_L0 + D_L1) + s_o S per
-//   32-block (s_t = d, s_o = -8 d for Q4_0; d, 0 for Q8_0; d sc, -dmin m for
-//   Q4_K).
-// Work split: one workgroup of 1024 threads per CU (grid = CU count); CU c
-// owns row tiles c, c + G, ...; wave w takes rounds w, w + 16, ... of each
-// tile; the per-wave partial sums meet in LDS in a fixed order. The first
-// part of x is loaded before any weight (see vx_gemv_p1).
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-#define VX_B_WG 1024
-
-// 1.5 * 2^23: fmaf(v, s, VX_RND_MAGIC) rounds v s to the nearest integer n
-// (ties to even) for |v s| < 2^22, leaving n - VX_RND_MAGIC exact and the
-// low byte of the float's bits equal to n & 0xFF (the int8 of n).
-#define VX_RND_MAGIC 12582912.0f
-
-// Low bytes of four floats from fmaf(., ., VX_RND_MAGIC), packed.
-__device__ __forceinline__ uint32_t vx_pack_lo_bytes(const float (&t)[4]) {
-    const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(t[1]), __float_as_uint(t[0]), 0x0C0C0400u);
-    const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(t[3]), __float_as_uint(t[2]), 0x04000C0Cu);
-    return lo | hi;
-}
-
-// B operand for piece s (elements 16s..16s+15) of a unit held in r.
-template <int QT, int S>
-__device__ __forceinline__ i32x4 vx_m_piece(const uint32_t (&r)[vx_unit<QT>::NW]) {
-    i32x4 b;
-    if constexpr (QT == VX_Q4_0) {
-        // block S/2: qs at byte 2 (block 0, dwords 0..4) or 20 (block 1,
-        // dwords 5..8); elements 0..15 low nibbles, 16..31 high nibbles.
-        constexpr int base = (S >> 1) ? 5 : 0;
-        constexpr uint32_t sh = ((S >> 1) ? 0u : 16u) + 4u * (S & 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t nx = (base + i + 1 <= 8) ? r[base + i + 1] : r[8];
-            b[i] = (int)(__builtin_amdgcn_alignbit(nx, r[base + i], sh) & 0x0F0F0F0Fu);
-        }
-    } else if constexpr (QT == VX_Q8_0) {
-        // block S/2 at byte 34 (S/2): elements 16(S&1).. at byte 2 + 16(S&1)
-        constexpr int base = (S >> 1) ? 9 + 4 * (S & 1) : 4 * (S & 1);
-        constexpr uint32_t sh = (S >> 1) ? 0u : 16u;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t nx = (base + i + 1 <= 16) ? r[base + i + 1] : r[16];
-            b[i] = (int)__builtin_amdgcn_alignbit(nx, r[base + i], sh);
-        }
-    } else {
-        // sub-block 2c + S/2: low (S/2 = 0) or high nibbles of qs bytes
-        // 16(S&1)..16(S&1)+15 of the quarter
-        constexpr int base = 4 + 4 * (S & 1);
-        constexpr uint32_t sh = 4u * (S >> 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            b[i] = (int)(__builtin_amdgcn_alignbit(r[base + i], r[base + i], sh) & 0x0F0F0F0Fu);
-    }
-    return b;
-}
-
-// Scale terms (s_t, s_o) of the two 32-blocks of a unit.
-template <int QT>
-__device__ __forceinline__ void vx_m_scales(const uint32_t (&r)[vx_unit<QT>::NW], uint32_t u, float (&st)[2],
-                                            float (&so)[2]) {
-    if constexpr (QT == VX_Q4_0) {
-        st[0] = vx_f16_to_f32(r[0]);
-        st[1] = vx_f16_to_f32(r[4] >> 16);
-        so[0] = -8.f * st[0];
-        so[1] = -8.f * st[1];
-    } else if constexpr (QT == VX_Q8_0) {
-        st[0] = vx_f16_to_f32(r[0]);
-        st[1] = vx_f16_to_f32(r[8] >> 16);
-        so[0] = 0.f;
-        so[1] = 0.f;
-    } else {
-        const float d = vx_f16_to_f32(r[0]);
-        const float dmin = vx_f16_to_f32(r[0] >> 16);
-        uint32_t sc0, m0, sc1, m1;
-        vx_q4k_scales(r[1], r[2], r[3], u & 3u, sc0, m0, sc1, m1);
-        st[0] = d * (float)sc0;
-        st[1] = d * (float)sc1;
-        so[0] = -(dmin * (float)m0);
-        so[1] = -(dmin * (float)m1);
-    }
-}
-
-template <int QT, int NCP, bool XV>
-__device__ __forceinline__ void vx_gemv_i8b(const vx_gemv_args& a) {
-    constexpr int NW = vx_unit<QT>::NW;
-    constexpr int NC = 2 * NCP;
-    const uint32_t t = threadIdx.x, lane = t & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t j = lane & 15u, o = lane >> 4;
-    const uint32_t G = gridDim.x, cu = blockIdx.x;
-    const uint32_t B = a.B;
-    const uint32_t nunits = a.nunits;
-    const uint32_t ntiles = (a.M + 15u) >> 4;
-    const uint32_t nts = ntiles > cu ? (ntiles - cu + G - 1u) / G : 0u;
-    const uint32_t rpt = (nunits + 3u) >> 2;  // rounds per tile
-    const uint32_t upw = (rpt + 15u) >> 4;    // round slots per wave per tile
-    const uint32_t nitems = nts * upw;
-
-    // LDS: xq [col][unit][2][64] int8 | scl [col][unit] {c2_0, S_0, c2_1,
-    // S_1} (S = sum of the block's x; -8 times that for Q4_0) | red [slot]
-    // [16 waves][col][16] | 64 zero bytes at a.upitch.
-    uint8_t* xq = (uint8_t*)vx_lds_x;
-    f32x4* scl = (f32x4*)(xq + 128u * B * nunits);
-    float* red = (float*)(scl + B * nunits);
-    if (t < 16u) ((uint32_t*)(xq + a.upitch))[t] = 0u;
-
-    // 1. x: block g = 32-block g % bpc of column g / bpc. Thread t splits
-    //    blocks t, t + 1024, ...; the first one is loaded before the
-    //    issue-order barrier.
-    const uint32_t bpc = 2u * nunits, nblk = B * bpc;
-    auto xload = [&](uint32_t g, f32x4 (&v)[8]) {
-        const uint32_t col = g / bpc, blk = g - col * bpc;
-        if constexpr (XV) {
-            const f32x4* xp = (const f32x4*)(a.x + (int64_t)col * a.xs_b + 32 * (int64_t)blk);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = xp[i];
-        } else {
-            const float* xp = a.x + (int64_t)col * a.xs_b + 32 * (int64_t)blk * a.xs_k;
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                v[i] = f32x4{xp[(4 * i) * a.xs_k], xp[(4 * i + 1) * a.xs_k], xp[(4 * i + 2) * a.xs_k],
-                             xp[(4 * i + 3) * a.xs_k]};
-        }
-    };
-    f32x4 xr[8];
-    xload(min(t, nblk - 1u), xr);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-
-    const uint32_t lrow = lane >> 2, lu = lane & 3u;
-    const uint32_t perm = 4u * (4u * j + o);
-    auto rowbase = [&](uint32_t ts) {
-        const uint32_t row = min((cu + ts * G) * 16u + lrow, a.M - 1u);
-        return a.w + (uint64_t)row * a.row_stride;
-    };
-    auto unit_of = [&](uint32_t k) { return min(4u * (wave + 16u * k) + lu, nunits - 1u); };
-    uint32_t pts = 0, pk = 0;
-    const uint8_t* prow = rowbase(0u);
-    auto padv = [&]() {
-        if (++pk == upw) {
-            pk = 0;
-            if (pts + 1u < nts) {
-                ++pts;
-                prow = rowbase(pts);
-            } else {
-                pk = upw - 1u;  // past the end: repeat the last item
-            }
-        }
-    };
-    uint32_t wr[2][NW];
-    vx_load_unit<QT>(prow, unit_of(0u), wr[0]);
-    padv();
-
-    // 2. split each block into two int8 levels: x ~= c2 (254 q1 + q2) with
-    //    c1 = max|x| / 126, c2 = c1 / 254, q1 = rnd(x / c1), q2 = rnd((x -
-    //    q1 c1) / c2); |x / c1 - q1| <= 1/2 (plus rounding of the reciprocal)
-    //    keeps |q2| <= 127. Blocks with max|x| < 2^-100 are stored as zero.
-    auto split = [&](uint32_t g, const f32x4 (&v)[8]) {
-        float m = 0.f, s4[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
-            s4[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
-        }
-        const float ps = ((s4[0] + s4[1]) + (s4[2] + s4[3])) + ((s4[4] + s4[5]) + (s4[6] + s4[7]));
-        const bool fin = m < __builtin_inff() && ps == ps;  // fmaxf skips NaN; the sum does not
-        const float c1 = m * (1.f / 126.f), c2 = c1 * (1.f / 254.f);
-        const float i1 = (fin && m >= 0x1p-100f) ? 126.f * __builtin_amdgcn_rcpf(m) : 0.f, i2 = i1 * 254.f;
-        uint32_t l0[8], l1[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float t1[4], t2[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                t1[e] = __builtin_fmaf(v[i][e], i1, VX_RND_MAGIC);
-                const float r1 = __builtin_fmaf(-(t1[e] - VX_RND_MAGIC), c1, v[i][e]);
-                t2[e] = __builtin_fmaf(r1, i2, VX_RND_MAGIC);
-            }
-            l0[i] = vx_pack_lo_bytes(t1);
-            l1[i] = vx_pack_lo_bytes(t2);
-        }
-        const uint32_t col = g / bpc, blk = g - col * bpc;
-        const uint32_t cu_ = col * nunits + (blk >> 1), h = blk & 1u;
-        uint4* xu = (uint4*)(xq + 128u * cu_ + 32u * h);
-        xu[0] = uint4{l0[0], l0[1], l0[2], l0[3]};
-        xu[1] = uint4{l0[4], l0[5], l0[6], l0[7]};
-        xu[4] = uint4{l1[0], l1[1], l1[2], l1[3]};
-        xu[5] = uint4{l1[4], l1[5], l1[6], l1[7]};
-        // Q4_0 keeps -8 sum(x): its block offset is then folded into one FMA
-        const float so_x = QT == VX_Q4_0 ? -8.f * ps : ps;
-        *(float2*)((float*)(scl + cu_) + 2u * h) = float2{fin ? c2 : m + ps, so_x};  // non-finite x: into y
-    };
-    if (t < nblk) split(t, xr);
-    for (uint32_t g = t + VX_B_WG; g < nblk; g += VX_B_WG) {
-        f32x4 v[8];
-        xload(g, v);
-        split(g, v);
-    }
-    __syncthreads();
-
-    // 3. rounds (ring of two).
-    vx_load_unit<QT>(prow, unit_of(pk), wr[1]);
-    padv();
-    const uint32_t ai = lane & 15u, ao = lane >> 4;
-    const bool a_on = (ai >> 2) == ao;
-    const uint32_t ac = (ai >> 1) & 1u, aL = ai & 1u;
-    const bool ragged = (nunits & 3u) != 0u;
-    float acc[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = 0.f;
-    i32x4 areg[NCP][2];
-#pragma unroll
-    for (int cp = 0; cp < NCP; ++cp) areg[cp][0] = areg[cp][1] = i32x4{0, 0, 0, 0};
-    uint32_t ts = 0, k = 0;
-    auto body = [&](uint32_t (&rl)[NW]) {
-        const uint32_t q = wave + 16u * k;  // round of this tile
-        if (q < rpt) {
-            uint32_t r[NW];
-#pragma unroll
-            for (int i = 0; i < NW; ++i) r[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)perm, (int)rl[i]);
-            const uint32_t u = min(4u * q + o, nunits - 1u);
-            const uint32_t ua = min(4u * q + ao, nunits - 1u);
-            uint32_t abase[NCP];
-#pragma unroll
-            for (int cp = 0; cp < NCP; ++cp) {
-                const uint32_t col = 2u * cp + ac;
-                abase[cp] = (a_on && col < B) ? (128u * (col * nunits + ua) + 64u * aL) : a.upitch;
-            }
-            // Pieces 2b and 2b + 1 share block b's scales: the second MFMA
-            // accumulates onto the first. Then per column c of the pair
-            // T = 254 D_L0 + D_L1 (|D| < 2^20: exact in int32).
-            const i32x4 z = i32x4{0, 0, 0, 0};
-            float tq[NCP][2][2];
-            // Only the 16 lanes inside their k-group's A rows load (columns >=
-            // B read the 64 zero bytes at a.upitch); the other lanes' A
-            // registers were zeroed once and are never written.
-#pragma unroll
-            for (int bb = 0; bb < 2; ++bb) {
-                if (a_on) {
-#pragma unroll
-                    for (int cp = 0; cp < NCP; ++cp) {
-                        const uint8_t* ap = xq + abase[cp] + 32u * bb;
-                        areg[cp][0] = *(const i32x4*)ap;
-                        areg[cp][1] = *(const i32x4*)(ap + 16u);
-                    }
-                }
-                const i32x4 bw0 = bb ? vx_m_piece<QT, 2>(r) : vx_m_piece<QT, 0>(r);
-                const i32x4 bw1 = bb ? vx_m_piece<QT, 3>(r) : vx_m_piece<QT, 1>(r);
-#pragma unroll
-                for (int cp = 0; cp < NCP; ++cp) {
-                    const i32x4 a0 = areg[cp][0];
-                    const i32x4 a1 = areg[cp][1];
-                    i32x4 dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bw0, z, 0, 0, 0);
-                    dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bw1, dd, 0, 0, 0);
-                    tq[cp][0][bb] = (float)(__mul24(dd[0], 254) + dd[1]);
-                    tq[cp][1][bb] = (float)(__mul24(dd[2], 254) + dd[3]);
-                }
-            }
-            float st[2], so[2];
-            vx_m_scales<QT>(r, u, st, so);
-            if (!(ragged && 4u * q + o >= nunits)) {
-#pragma unroll
-                for (int cp = 0; cp < NCP; ++cp)
-#pragma unroll
-                    for (int c = 0; c < 2; ++c) {
-                        const uint32_t col = 2u * cp + c;
-                        if (col < B) {
-                            const f32x4 sc = scl[col * nunits + u];
-                            float v = acc[2 * cp + c];
-                            if constexpr (QT == VX_Q4_0) {
-                                // d (c2 T - 8 sum x): the block scale times its int dot
-                                // minus the offset of the biased nibbles
-                                v = __builtin_fmaf(st[0], __builtin_fmaf(sc.x, tq[cp][c][0], sc.y), v);
-                                v = __builtin_fmaf(st[1], __builtin_fmaf(sc.z, tq[cp][c][1], sc.w), v);
-                            } else {
-                                v = __builtin_fmaf(st[0], sc.x * tq[cp][c][0], v);
-                                v = __builtin_fmaf(st[1], sc.z * tq[cp][c][1], v);
-                                if constexpr (QT != VX_Q8_0) {
-                                    v = __builtin_fmaf(so[0], sc.y, v);
-                                    v = __builtin_fmaf(so[1], sc.w, v);
-                                }
-                            }
-                            acc[2 * cp + c] = v;
-                        }
-                    }
-            }
-        }
-        vx_load_unit<QT>(prow, unit_of(pk), rl);
-        padv();
-        if (++k == upw) {
-            // row j's sums over the four units of this wave's rounds, four
-            // columns at a time: row r of the result is column c0 + r
-#pragma unroll
-            for (int c0 = 0; c0 < NC; c0 += 4) {
-                const float v = vx_sum_rows4x4(acc[c0], acc[c0 + 1], c0 + 2 < NC ? acc[c0 + 2] : 0.f,
-                                               c0 + 3 < NC ? acc[c0 + 3] : 0.f);
-                if ((uint32_t)c0 + (lane >> 4) < B) red[((ts * 16u + wave) * B + (uint32_t)c0) * 16u + lane] = v;
-            }
-#pragma unroll
-            for (int c = 0; c < NC; ++c) acc[c] = 0.f;
-            k = 0;
-            ++ts;
-        }
-    };
-    const uint32_t nfull = nitems & ~1u;
-    for (uint32_t it0 = 0; it0 < nfull; it0 += 2) {
-        body(wr[0]);
-        body(wr[1]);
-    }
-    if (nfull < nitems) body(wr[0]);
-
-    // 4. per tile, row and column: sum the 16 waves in a fixed order.
-    __syncthreads();
-    for (uint32_t idx = t; idx < nts * 16u * B; idx += VX_B_WG) {
-        const uint32_t ts2 = idx / (16u * B), rem = idx - ts2 * 16u * B;
-        const uint32_t col = rem >> 4, jj = rem & 15u;
-        const uint32_t row = (cu + ts2 * G) * 16u + jj;
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) sum += red[((ts2 * 16u + w) * B + col) * 16u + jj];
-        if (row < a.M) a.y[(int64_t)row * a.ys_m + (int64_t)col * a.ys_b] = sum;
-    }
-}
 
 // Any layout fallback (K a multiple of 32, any alignment, any B): one
 // wave per row, lane l decodes 32-weight groups l, l+64, ... byte by byte.
@@ -1194,10 +853,6 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(vx_gemv_args a) {  \
         if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true>(a); else vx_gemv_p1i<QT, P, 1024, false>(a); \
     }
-#define VX_GEMV_I8B(QT, QN, NCP)                                                                \
-    extern "C" __global__ __launch_bounds__(VX_B_WG) void vx_gemv_i8b_##QN##_c##NCP(vx_gemv_args a) { \
-        if (a.x_vec) vx_gemv_i8b<QT, NCP, true>(a); else vx_gemv_i8b<QT, NCP, false>(a);        \
-    }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
     VX_GEMV_B1(QT, QN, 2)                                                                           \
@@ -1226,15 +881,6 @@ VX_GEMV_P1I(VX_Q4_0, q4_0, 2)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
-VX_GEMV_I8B(VX_Q4_0, q4_0, 1)
-VX_GEMV_I8B(VX_Q4_0, q4_0, 2)
-VX_GEMV_I8B(VX_Q4_0, q4_0, 4)
-VX_GEMV_I8B(VX_Q8_0, q8_0, 1)
-VX_GEMV_I8B(VX_Q8_0, q8_0, 2)
-VX_GEMV_I8B(VX_Q8_0, q8_0, 4)
-VX_GEMV_I8B(VX_Q4_K, q4_k, 1)
-VX_GEMV_I8B(VX_Q4_K, q4_k, 2)
-VX_GEMV_I8B(VX_Q4_K, q4_k, 4)
 
 // ------------------------------------------------------------------------
 // Batched GEMV on split activations (vx_xq, written once per call by

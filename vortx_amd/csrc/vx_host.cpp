@@ -355,7 +355,12 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
         g.y_bs[1] = p.o.l.stride[1];
         g.alpha = alpha;
         g.beta = beta;
-        return launch(ctx, K_vx_gemv_f32, dim3((p.M + 3) / 4, batch, 1), dim3(VX_WG), 0, stream, g);
+        // one row per workgroup, or four when a row is short (K < 4096: then
+        // one row would leave each wave fewer than four loads in flight)
+        // (a grid holds fewer than 2^32 threads: 2^24 one-row workgroups)
+        if (p.K >= 4096u && p.M < (1u << 24))
+            return launch(ctx, K_vx_gemv_f32, dim3(p.M, batch, 1), dim3(VX_WG), 0, stream, g);
+        return launch(ctx, K_vx_gemv_f32_r4, dim3((p.M + 3) / 4, batch, 1), dim3(VX_WG), 0, stream, g);
     }
     vx_gemm_args a{};
     a.c = (float*)p.o.ptr;
@@ -475,22 +480,6 @@ static int p1i_kernel(uint32_t qt, int P) {
     case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
     default: return K_vx_gemv_p1i_q4_k_p2;
     }
-}
-
-static int i8b_kernel(uint32_t qt, uint32_t B) {
-    static const int tab[3][3] = {
-        {K_vx_gemv_i8b_q4_0_c1, K_vx_gemv_i8b_q4_0_c2, K_vx_gemv_i8b_q4_0_c4},
-        {K_vx_gemv_i8b_q8_0_c1, K_vx_gemv_i8b_q8_0_c2, K_vx_gemv_i8b_q8_0_c4},
-        {K_vx_gemv_i8b_q4_k_c1, K_vx_gemv_i8b_q4_k_c2, K_vx_gemv_i8b_q4_k_c4}};
-    return tab[q_index(qt)][B <= 2 ? 0 : B <= 4 ? 1 : 2];
-}
-
-// LDS bytes of the int8 matrix-core batched kernel for B columns: x levels
-// (128 B per unit and column), block scales (16 B per unit and column),
-// per-wave partial sums (1 KB per row tile of the CU and column), 64 zero
-// bytes.
-static size_t i8b_lds(uint32_t B, uint32_t nunits, uint32_t nts) {
-    return (size_t)144u * B * nunits + (size_t)1024u * B * nts + 64u;
 }
 
 static int generic_kernel(uint32_t qt) {
@@ -765,28 +754,6 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         }
         if ((s = launch_quantize_x(ctx, stream, &q, cx))) return s;
         return launch_gemv_xq(ctx, stream, cy, w, &q);
-    }
-    if (B >= 2 && fast && !force_simt) {
-        // int8 matrix-core path, one workgroup per CU, up to 8 columns per
-        // launch (fewer when x of that many columns does not fit LDS).
-        const uint32_t nts = ((M + 15u) / 16u + (uint32_t)ctx->num_cus - 1u) / (uint32_t)ctx->num_cus;
-        uint32_t cpl = 8u;
-        while (cpl > 1u && i8b_lds(cpl < B ? cpl : B, a.nunits, nts) > budget) cpl >>= 1;
-        if (cpl >= 2u || i8b_lds(1u, a.nunits, nts) <= budget) {
-            for (uint32_t b0 = 0; b0 < B; b0 += cpl) {
-                a.B = B - b0 < cpl ? B - b0 : cpl;
-                a.x = (const float*)(cx.ptr + 4ull * (uint64_t)b0 * (uint64_t)cx.l.stride[3]);
-                a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
-                a.x_vec = (a.xs_k == 1 && aligned16((uintptr_t)a.x) && (a.B == 1 || a.xs_b % 4 == 0)) ? 1u : 0u;
-                a.chunk_units = a.nunits;
-                a.upitch = (uint32_t)(i8b_lds(a.B, a.nunits, nts) - 64u);  // zero area offset
-                size_t lds = i8b_lds(a.B, a.nunits, nts);
-                if (lds < 82u * 1024u) lds = budget < 82u * 1024u ? budget : 82u * 1024u;
-                s = launch(ctx, i8b_kernel(w->qtype, a.B), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
-                if (s) return s;
-            }
-            return VX_OK;
-        }
     }
     // batch-1 kernel: the persistent one, or the per-row-group one when x
     // does not fit the persistent kernel's LDS (K > 16384); int8 x unless
