@@ -156,12 +156,14 @@ typedef enum vx_gemm_flags {
      * of TensorLayout::broadcast (src/shapes.rs:346-391) that the reference
      * leaves as a TODO in Gemm::dispatch (src/linalg/gemm.rs:64). */
     VX_GEMM_BROADCAST = 1,
-    /* Tile shape of the MFMA kernel, for callers that pin it (both give the
-     * same bits; by default the one that fills the GPU's last round of
-     * resident workgroups better is taken): 128 x 128 or 128 x 256 output
-     * tiles. Exclusive; ignored on the naive and GEMV routes. */
+    /* Tile shape of the MFMA kernel, for callers that pin it (all give the
+     * same bits; by default the one that fills the GPU best is taken):
+     * 128 x 128, 128 x 256 or 64 x 64 output tiles. Exclusive; ignored on
+     * the naive and GEMV routes; WIDE and SMALL apply to operands whose A is
+     * contiguous along K and B along K or N (others keep 128 x 128). */
     VX_GEMM_TILE_NARROW = 2,
-    VX_GEMM_TILE_WIDE = 4
+    VX_GEMM_TILE_WIDE = 4,
+    VX_GEMM_TILE_SMALL = 8
 } vx_gemm_flags;
 
 typedef struct vx_gemm_opts {

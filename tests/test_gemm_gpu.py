@@ -75,19 +75,23 @@ def test_tiled_parity(gemm, M, N, K):
                                         (300, 517, 129, False), (513, 1000, 100, True), (1024, 1024, 1024, False)])
 def test_wide_tiles_match_narrow(gemm, M, N, K, tr_b):
     """The 128 x 256 tile kernels (chosen for shapes such as 4096^3, forced
-    here with VX_GEMM_TILE_WIDE) give the same bits as the 128 x 128 ones
-    (VX_GEMM_TILE_NARROW) and as the default choice: each output is the same
-    sum in the same order. Edge tiles in M, N and K."""
+    here with VX_GEMM_TILE_WIDE) and the 64 x 64 ones (chosen when the
+    128 x 128 tiles are fewer than the CUs, e.g. 1024^3; VX_GEMM_TILE_SMALL)
+    give the same bits as the 128 x 128 ones (VX_GEMM_TILE_NARROW) and as the
+    default choice: each output is the same sum in the same order. Edge tiles
+    in M, N and K."""
     note(f"wide tiles {M}x{N}x{K} trB={tr_b}")
     a = S.uniform((M, K), 5, DEV)
     b = S.uniform((N, K), 6, DEV).t() if tr_b else S.uniform((K, N), 6, DEV)
-    c0, c1, c2 = _nan(M, N), _nan(M, N), _nan(M, N)
+    c0, c1, c2, c3 = _nan(M, N), _nan(M, N), _nan(M, N), _nan(M, N)
     gemm.dispatch_ex(c0, a, b, tile="narrow")
     gemm.dispatch_ex(c1, a, b, tile="wide")
     gemm.dispatch(c2, a, b)
+    gemm.dispatch_ex(c3, a, b, tile="small")
     torch.cuda.synchronize()
     assert torch.equal(c0.view(torch.int32), c1.view(torch.int32))
     assert torch.equal(c0.view(torch.int32), c2.view(torch.int32))
+    assert torch.equal(c0.view(torch.int32), c3.view(torch.int32))
     assert_close(c1.cpu().numpy(), _f64(a, b.contiguous())[0, 0])
 
 

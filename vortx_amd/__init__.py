@@ -200,11 +200,12 @@ class Gemm(_Context):
         """out = alpha * (lhs x rhs) + beta * out (vx_gemm_f32_ex); out is not
         read when beta == 0. ``broadcast``: batch dims of lhs / rhs of size 1
         are reused along out's (src/shapes.rs:346-391 semantics). ``tile``:
-        "narrow" / "wide" pins the MFMA kernel's 128 x 128 / 128 x 256 output
-        tiles (same bits either way), "auto" lets the library choose."""
+        "narrow" / "wide" / "small" pins the MFMA kernel's 128 x 128 / 128 x 256 /
+        64 x 64 output tiles (same bits every way), "auto" lets the library choose."""
         o, l, r = _view_of(out, True), _view_of(lhs, False), _view_of(rhs, False)
         flags = (_ffi.VX_GEMM_BROADCAST if broadcast else 0) | {"auto": 0, "narrow": _ffi.VX_GEMM_TILE_NARROW,
-                                                                 "wide": _ffi.VX_GEMM_TILE_WIDE}[tile]
+                                                                 "wide": _ffi.VX_GEMM_TILE_WIDE,
+                                                                 "small": _ffi.VX_GEMM_TILE_SMALL}[tile]
         opts = _ffi.VxGemmOpts(alpha, beta, flags, 0)
         check(lib().vx_gemm_f32_ex(self._h, _stream(stream), C.byref(o), C.byref(l), C.byref(r), C.byref(opts)))
 

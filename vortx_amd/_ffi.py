@@ -44,7 +44,7 @@ class VxGemmOpts(C.Structure):
     _fields_ = [("alpha", C.c_float), ("beta", C.c_float), ("flags", C.c_uint32), ("reserved", C.c_uint32)]
 
 
-VX_GEMM_BROADCAST, VX_GEMM_TILE_NARROW, VX_GEMM_TILE_WIDE = 1, 2, 4
+VX_GEMM_BROADCAST, VX_GEMM_TILE_NARROW, VX_GEMM_TILE_WIDE, VX_GEMM_TILE_SMALL = 1, 2, 4, 8
 
 
 class VxGgufHeader(C.Structure):

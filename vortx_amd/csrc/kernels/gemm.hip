@@ -26,12 +26,8 @@
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-#define TBM 128
-#define TBN 128
 #define TBK 16
 #define LDS_PAD 4
-#define LDA_S (TBM + LDS_PAD)
-#define LDB_S (TBN + LDS_PAD)
 
 // Operand access modes (chosen on the host from strides and alignment).
 #define MODE_KC 0  // contiguous along K, rows 16-byte aligned
@@ -183,10 +179,11 @@ __device__ __forceinline__ void vx_store_frag(const vx_frag<MODE, TX>& f, float*
     }
 }
 
-template <int AMODE, int BMODE, int TN>
+template <int AMODE, int BMODE, int TM, int TN>
 __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
-    constexpr int LDB = TN + LDS_PAD, NJ = TN / 64;  // per wave: 64 x TN / 2, NJ column blocks
-    __shared__ float As[2][TBK * LDA_S];
+    // per wave: TM / 2 x TN / 2, MI row and NJ column blocks of 32
+    constexpr int LDA = TM + LDS_PAD, LDB = TN + LDS_PAD, MI = TM / 64, NJ = TN / 64;
+    __shared__ float As[2][TBK * LDA];
     __shared__ float Bs[2][TBK * LDB];
 
     // Tile order: consecutive workgroup ids land on different XCDs (round
@@ -201,7 +198,7 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     const uint32_t gsize = min(p.tiles_m - first_m, 8u);
     const uint32_t tm = first_m + (bid % group) % gsize;
     const uint32_t tn = (bid % group) / gsize;
-    const uint32_t m0 = tm * TBM, n0 = tn * TN;
+    const uint32_t m0 = tm * TM, n0 = tn * TN;
 
     const uint32_t z = blockIdx.z;
     const uint32_t bn = z / p.batch_c, bc = z % p.batch_c;
@@ -213,9 +210,9 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     const uint32_t wm = wave >> 1, wn = wave & 1u;
     const uint32_t l32 = lane & 31u, lk = lane >> 5;
 
-    f32x16 acc[2][NJ];
+    f32x16 acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -223,41 +220,42 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 
     // One TBK stage from LDS buffer `buf`.
     auto mma = [&](uint32_t buf) {
-        const float* as = As[buf] + wm * 64u + l32;
+        const float* as = As[buf] + wm * (TM / 2u) + l32;
         const float* bs = Bs[buf] + wn * (TN / 2u) + l32;
 #pragma unroll
         for (int ks = 0; ks < TBK / 2; ++ks) {
             const uint32_t kk = 2u * ks + lk;
-            const float a0 = as[kk * LDA_S], a1 = as[kk * LDA_S + 32];
-            float b[NJ];
+            float a[MI], b[NJ];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) a[i] = as[kk * LDA + 32 * i];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) b[j] = bs[kk * LDB + 32 * j];
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b[j], acc[0][j], 0, 0, 0);
-                acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b[j], acc[1][j], 0, 0, 0);
-            }
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     };
 
     const uint32_t nkf = p.K / TBK;  // whole stages
-    if (m0 + TBM <= p.M && n0 + TN <= p.N) {
+    if (m0 + TM <= p.M && n0 + TN <= p.N) {
         // Tile inside M and N: the loads for stage s + 2 are issued while
         // stage s is multiplied (two register buffers), so each load has two
         // stages of MFMAs to arrive before its LDS store waits for it. Stage
         // indices are clamped to the last whole stage (the extra loads at the
         // end are harmless). Unrolled by two so each buffer is named.
         if (nkf) {
-            vx_frag<AMODE, TBM> ra0, ra1;
+            vx_frag<AMODE, TM> ra0, ra1;
             vx_frag<BMODE, TN> rb0, rb1;
-            auto ld = [&](uint32_t st, vx_frag<AMODE, TBM>& fa_, vx_frag<BMODE, TN>& fb_) {
+            auto ld = [&](uint32_t st, vx_frag<AMODE, TM>& fa_, vx_frag<BMODE, TN>& fb_) {
                 const uint32_t k0 = min(st, nkf - 1u) * TBK;
-                vx_load_frag_full<AMODE, TBM>(fa_, A, p.as[2], p.as[3], m0, k0);
+                vx_load_frag_full<AMODE, TM>(fa_, A, p.as[2], p.as[3], m0, k0);
                 vx_load_frag_full<BMODE, TN>(fb_, B, p.bs[3], p.bs[2], n0, k0);
             };
             ld(0u, ra0, rb0);
             ld(1u, ra1, rb1);
-            vx_store_frag<AMODE, TBM, LDA_S>(ra0, As[0]);
+            vx_store_frag<AMODE, TM, LDA>(ra0, As[0]);
             vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
             __syncthreads();
             // Invariant at the top: stage st in buffer 0, stage st + 1 in
@@ -269,13 +267,13 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
                 // below the other buffer's store and share its registers)
                 __builtin_amdgcn_sched_barrier(0);
                 mma(0u);
-                vx_store_frag<AMODE, TBM, LDA_S>(ra1, As[1]);
+                vx_store_frag<AMODE, TM, LDA>(ra1, As[1]);
                 vx_store_frag<BMODE, TN, LDB>(rb1, Bs[1]);
                 __syncthreads();
                 ld(st + 3u, ra1, rb1);
                 __builtin_amdgcn_sched_barrier(0);
                 mma(1u);
-                vx_store_frag<AMODE, TBM, LDA_S>(ra0, As[0]);
+                vx_store_frag<AMODE, TM, LDA>(ra0, As[0]);
                 vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
                 __syncthreads();
             }
@@ -284,24 +282,24 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
         if (p.K % TBK) {
             // the K tail: one stage zero-filled past K, through buffer 1
             // (its last reader finished before a barrier)
-            vx_frag<AMODE, TBM> fa;
+            vx_frag<AMODE, TM> fa;
             vx_frag<BMODE, TN> fb;
-            vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, nkf * TBK, p.K);
+            vx_load_frag<AMODE, TM>(fa, A, p.as[2], p.as[3], m0, p.M, nkf * TBK, p.K);
             vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, nkf * TBK, p.K);
-            vx_store_frag<AMODE, TBM, LDA_S>(fa, As[1]);
+            vx_store_frag<AMODE, TM, LDA>(fa, As[1]);
             vx_store_frag<BMODE, TN, LDB>(fb, Bs[1]);
             __syncthreads();
             mma(1u);
         }
     } else {
         // Edge tile: zero-filled loads of the next stage during this one.
-        vx_frag<AMODE, TBM> fa;
+        vx_frag<AMODE, TM> fa;
         vx_frag<BMODE, TN> fb;
         const uint32_t nk = (p.K + TBK - 1) / TBK;
         if (nk) {
-            vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
+            vx_load_frag<AMODE, TM>(fa, A, p.as[2], p.as[3], m0, p.M, 0, p.K);
             vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, 0, p.K);
-            vx_store_frag<AMODE, TBM, LDA_S>(fa, As[0]);
+            vx_store_frag<AMODE, TM, LDA>(fa, As[0]);
             vx_store_frag<BMODE, TN, LDB>(fb, Bs[0]);
             __syncthreads();
         }
@@ -309,12 +307,12 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
             const uint32_t cur = kt & 1u;
             const bool more = kt + 1 < nk;
             if (more) {
-                vx_load_frag<AMODE, TBM>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
+                vx_load_frag<AMODE, TM>(fa, A, p.as[2], p.as[3], m0, p.M, (kt + 1) * TBK, p.K);
                 vx_load_frag<BMODE, TN>(fb, B, p.bs[3], p.bs[2], n0, p.N, (kt + 1) * TBK, p.K);
             }
             mma(cur);
             if (more) {
-                vx_store_frag<AMODE, TBM, LDA_S>(fa, As[cur ^ 1u]);
+                vx_store_frag<AMODE, TM, LDA>(fa, As[cur ^ 1u]);
                 vx_store_frag<BMODE, TN, LDB>(fb, Bs[cur ^ 1u]);
             }
             __syncthreads();
@@ -324,13 +322,13 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
     // D layout of v_mfma_f32_32x32x2f32: register v of lane l holds
     // row 8*(v/4) + 4*(l/32) + v%4, column l%32 of the 32x32 tile.
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             const uint32_t col = n0 + wn * (TN / 2u) + 32u * j + l32;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const uint32_t row = m0 + wm * 64u + 32u * i + 8u * (v >> 2) + 4u * lk + (v & 3);
+                const uint32_t row = m0 + wm * (TM / 2u) + 32u * i + 8u * (v >> 2) + 4u * lk + (v & 3);
                 if (row < p.M && col < p.N)
                     vx_epilogue(Cp + (int64_t)row * p.cs[2] + (int64_t)col * p.cs[3], acc[i][j][v], p.alpha, p.beta);
             }
@@ -346,12 +344,19 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
 #define VX_GEMM_MFMA(AM, BM, NAME, WPE)                                                              \
     extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(WPE, 4)))    \
     void vx_gemm_mfma_##NAME(vx_gemm_args p) {                                                       \
-        vx_gemm_mfma<AM, BM, 128>(p);                                                                \
+        vx_gemm_mfma<AM, BM, 128, 128>(p);                                                              \
     }
 #define VX_GEMM_MFMA_W(AM, BM, NAME)                                                                 \
     extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(2, 2)))      \
     void vx_gemm_mfma_##NAME##_w(vx_gemm_args p) {                                                   \
-        vx_gemm_mfma<AM, BM, 256>(p);                                                                \
+        vx_gemm_mfma<AM, BM, 128, 256>(p);                                                              \
+    }
+// 64 x 64 tiles (each wave 32 x 32, one accumulator) for shapes with fewer
+// 128 x 128 tiles than CUs: 1024^3 is 64 such tiles but 256 small ones.
+#define VX_GEMM_MFMA_S(AM, BM, NAME)                                                                 \
+    extern "C" __global__ __launch_bounds__(VX_WG) __attribute__((amdgpu_waves_per_eu(4, 8)))      \
+    void vx_gemm_mfma_##NAME##_s(vx_gemm_args p) {                                                   \
+        vx_gemm_mfma<AM, BM, 64, 64>(p);                                                             \
     }
 // Suffix letters: A mode then B mode; k = contiguous along K,
 // x = contiguous along M / N, g = generic.
@@ -364,6 +369,8 @@ VX_GEMM_MFMA(MODE_KC, MODE_GEN, kg, 3)
 VX_GEMM_MFMA(MODE_GEN, MODE_XC, gx, 3)
 VX_GEMM_MFMA_W(MODE_KC, MODE_XC, kx)
 VX_GEMM_MFMA_W(MODE_KC, MODE_KC, kk)
+VX_GEMM_MFMA_S(MODE_KC, MODE_XC, kx)
+VX_GEMM_MFMA_S(MODE_KC, MODE_KC, kk)
 
 // ---------------------------------------------------------------- gemv
 // y[m] = sum_k A[m, k] x[k]; A contiguous along K with 16-byte aligned
