@@ -73,7 +73,43 @@ def load_traffic(name: str):
     return None
 
 
+def graph_time(launch, steps: int):
+    """Capture min(steps, 500) launches (launch(i, stream)) into a HIP graph
+    on a side stream and replay it steps // that many times between two
+    synchronizations. Returns (launches done, wall seconds, HIP-event ms on
+    the stream the kernels run on)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    chunk = min(steps, 500)
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(chunk):
+                launch(i, s)
+    torch.cuda.synchronize()
+    reps = max(1, steps // chunk)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):  # replay() launches on the current stream
+        graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(s)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return reps * chunk, wall, e0.elapsed_time(e1)
+
+
 def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str, x_f32: bool = False):
+    """One step = vx_gemv_q on the next of >= 512 MB of weight copies
+    (K launches captured into a HIP graph and replayed; HIP events on the
+    graph's stream bracket the timed region). At B >= 2 on the default int8-x
+    path a step is two launches (vx_quantize_x, then vx_gemv_xq); the GEMV
+    kernel is then also timed alone, on a ready split, for the roofline."""
     import torch
 
     import vortx_amd as vx
@@ -96,43 +132,21 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     for i in range(warmup):
         g.dispatch(yv, qws[i % ncopy], xv, x_f32=x_f32)
     torch.cuda.synchronize()
-
-    # K launches captured once into a HIP graph (chunks of <= 500 nodes) on
-    # stream s and replayed; HIP events on s bracket the timed region, so
-    # their elapsed time / launches is the average launch duration of the
-    # kernel (back-to-back in one stream, gaps included).
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    chunk = min(steps, 500)
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(chunk):
-                g.dispatch(yv, qws[i % ncopy], xv, stream=s, x_f32=x_f32)
-    torch.cuda.synchronize()
-    reps = max(1, steps // chunk)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):  # replay() launches on the current stream
-        graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(s)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(s)
-        torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    done = reps * chunk
-    avg_launch_ms = e0.elapsed_time(e1) / done
+    done, wall, ev_ms = graph_time(lambda i, s: g.dispatch(yv, qws[i % ncopy], xv, stream=s, x_f32=x_f32), steps)
     alg = gemv_bytes(qtype, M, K, B)
-    return {
-        "steps": done,
-        "ms_per_step": wall * 1e3 / done,
-        "value": alg * done / wall / 1e9,
-        "avg_launch_ms": avg_launch_ms,
-        "alg_bytes": alg,
-        "weight_copies": ncopy,
-    }
+    r = {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
+         "avg_launch_ms": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
+    if B >= 2 and not x_f32:
+        q = vx.XQ.empty(K, B)
+        g.quantize_x(q, xv)
+        for i in range(min(warmup, 20)):
+            g.dispatch_xq(yv, qws[i % ncopy], q)
+        torch.cuda.synchronize()
+        n2, _, ev2 = graph_time(lambda i, s: g.dispatch_xq(yv, qws[i % ncopy], q, stream=s), steps)
+        r["launches_per_step"] = 2
+        r["step_ms_events"] = r["avg_launch_ms"]
+        r["avg_launch_ms"] = ev2 / n2  # the dominant kernel (vx_gemv_xq) alone
+    return r
 
 
 def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
@@ -491,12 +505,89 @@ def cpu_baselines_child(threads: int):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+# Batched and secondary GEMV configs: key -> (qtype, M, K, B, workload).
+GEMV_SECONDARY = {
+    "gemv_q8_0_4096x4096_b1": (8, 4096, 4096, 1, "Q8_0 GEMV 4096x4096 batch 1"),
+    "gemv_q4_k_32000x4096_b1": (12, 32000, 4096, 1, "Q4_K GEMV 32000x4096 batch 1"),
+    "gemv_q4_0_4096x11008_b1": (2, 4096, 11008, 1, "Q4_0 GEMV 4096x11008 batch 1"),
+    "gemv_q4_k_14336x4096_b1": (12, 14336, 4096, 1, "Q4_K GEMV 14336x4096 batch 1"),
+    "gemv_q4_0_11008x4096_b4": (2, 11008, 4096, 4, "Q4_0 GEMV 11008x4096 batch 4"),
+    "gemv_q4_0_11008x4096_b8": (2, 11008, 4096, 8, "Q4_0 GEMV 11008x4096 batch 8"),
+    "gemv_q4_0_4096x11008_b4": (2, 4096, 11008, 4, "Q4_0 GEMV 4096x11008 batch 4"),
+    "gemv_q4_0_4096x11008_b8": (2, 4096, 11008, 8, "Q4_0 GEMV 4096x11008 batch 8"),
+    "gemv_q8_0_4096x4096_b8": (8, 4096, 4096, 8, "Q8_0 GEMV 4096x4096 batch 8"),
+    "gemv_q4_k_14336x4096_b16": (12, 14336, 4096, 16, "Q4_K GEMV 14336x4096 batch 16"),
+    "gemv_q4_k_32000x4096_b16": (12, 32000, 4096, 16, "Q4_K GEMV 32000x4096 batch 16"),
+}
+GEMMS = {  # key -> (M, N, K, transb, workload)
+    "gemm_f32_4096": (4096, 4096, 4096, False, "f32 GEMM 4096^3 (row-major A, B)"),
+    "gemm_f32_4096x11008x4096": (4096, 11008, 4096, False, "f32 GEMM M=4096 N=11008 K=4096 (row-major A, B)"),
+    "gemm_f32_4096_transb": (4096, 4096, 4096, True, "f32 GEMM 4096^3, B a transposed view of a row-major [N, K] buffer"),
+}
+# every workload in run order (the keys --only selects from)
+KEYS = (["gemv_q4_0_11008x4096_b1", "gemv_q4_0_11008x4096_b1_f32x"] + list(GEMV_SECONDARY) +
+        ["gemv_f32_11008x4096", "gemv_f32_1552x4096", "gemv_f32_32768x4096", "gemm_sweep"] + list(GEMMS) +
+        ["gemm_f32_broadcast_8x1024", "contiguous_t8192", "copy_8192", "copy_3104x1024", "quantize_q8_0_14336x4096",
+         "quantize_q4_k_14336x4096", "gguf_upload"])
+
+
+def run_workloads(keys, steps: int, warmup: int) -> dict:
+    """Run the named workloads in KEYS order; returns key -> result."""
+    out = {}
+    gsteps, gwarm = max(5, min(50, steps // 40)), max(2, warmup // 100)
+    for k in [k for k in KEYS if k in keys]:
+        if k == "gemv_q4_0_11008x4096_b1":
+            r = time_gemv(2, 11008, 4096, 1, steps, warmup, "q4_0")
+        elif k == "gemv_q4_0_11008x4096_b1_f32x":
+            # the headline config with x kept in f32 (VX_GEMV_X_F32): f32 FMA on
+            # the exactly decoded weights, the exact-arithmetic twin of the default
+            r = time_gemv(2, 11008, 4096, 1, steps, warmup, "q4_0_f32x", x_f32=True)
+        elif k in GEMV_SECONDARY:
+            qt, M, K, B, _ = GEMV_SECONDARY[k]
+            r = time_gemv(qt, M, K, B, max(100, steps // (2 if B > 1 or M > 20000 else 1)), warmup, k)
+        elif k == "gemv_f32_11008x4096":
+            r = time_gemv_f32(11008, 4096, max(100, steps // 4), warmup)
+        elif k == "gemv_f32_1552x4096":
+            # a read-only stream of the headline's size: 1552 x 4096 f32 = 25.43 MB
+            # (the Q4_0 GEMV moves 25.42 MB)
+            r = time_gemv_f32(1552, 4096, steps, warmup)
+        elif k == "gemv_f32_32768x4096":
+            r = time_gemv_f32(32768, 4096, max(50, steps // 20), max(5, warmup // 20))
+        elif k == "gemm_sweep":
+            r = time_gemm_sweep()
+        elif k in GEMMS:
+            M, N, K, tb, _ = GEMMS[k]
+            r = time_gemm(M, N, K, gsteps, gwarm, transb=tb)
+        elif k == "gemm_f32_broadcast_8x1024":
+            r = time_gemm_broadcast(8, 1024, 4096, 4096, gsteps, gwarm)
+        elif k == "contiguous_t8192":
+            r = time_contiguous((8192, 8192), max(10, steps // 20), 5)
+        elif k == "copy_8192":
+            r = time_contiguous((8192, 8192), max(10, steps // 20), 5, transposed=False)
+        elif k == "copy_3104x1024":
+            # one launch moving the headline GEMV's bytes (25,422,848 / 8 elements,
+            # rounded up to whole rows of 1024)
+            r = time_copy_like_gemv(3104 * 1024, steps, warmup)
+        elif k == "quantize_q8_0_14336x4096":
+            r = time_quantize(8, 14336, 4096, max(10, steps // 20), 3)
+        elif k == "quantize_q4_k_14336x4096":
+            r = time_quantize(12, 14336, 4096, max(10, steps // 100), 3)
+        else:  # gguf_upload
+            r = time_gguf_upload(5)
+        log(f"[{k}] {r}")
+        out[k] = r
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", metavar="KEYS",
+                    help="comma-separated workload keys (profiling runs): print their raw results, not the "
+                         "benchmark line; keys: " + ", ".join(KEYS))
     ap.add_argument("--cpu-baseline-only", type=int, default=0, metavar="THREADS",
                     help=argparse.SUPPRESS)  # the CPU leg's own process: print its JSON and exit
     args = ap.parse_args()
@@ -512,83 +603,47 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.only:
+        keys = [k for k in args.only.split(",") if k]
+        bad = [k for k in keys if k not in KEYS]
+        if bad:
+            print(f"unknown workload keys {bad}; known: {KEYS}", file=sys.stderr)
+            return 2
+        print(json.dumps({"only": run_workloads(keys, args.steps, args.warmup)}), flush=True)
+        return 0
 
-    q40 = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0")
-    log(f"[q4_0] {q40}")
-    # The same headline config with x kept in f32 (VX_GEMV_X_F32): f32 FMA on
-    # the exactly decoded weights, the exact-arithmetic twin of the default.
-    q40f = time_gemv(2, 11008, 4096, 1, args.steps, args.warmup, "q4_0_f32x", x_f32=True)
-    log(f"[q4_0_f32x] {q40f}")
-    # secondary GEMV configs: (qtype, M, K, B, label, workload, traffic profile)
-    SECONDARY = [
-        (8, 4096, 4096, 1, "q8_0", "Q8_0 GEMV 4096x4096 batch 1", "gemv_q8_0_4096x4096_b1"),
-        (12, 32000, 4096, 1, "q4_k", "Q4_K GEMV 32000x4096 batch 1", "gemv_q4_k_32000x4096_b1"),
-        (2, 4096, 11008, 1, "q4_0_t", "Q4_0 GEMV 4096x11008 batch 1", "gemv_q4_0_4096x11008_b1"),
-        (12, 14336, 4096, 1, "q4_k_14336", "Q4_K GEMV 14336x4096 batch 1", "gemv_q4_k_14336x4096_b1"),
-        (2, 11008, 4096, 4, "q4_0_b4", "Q4_0 GEMV 11008x4096 batch 4", "gemv_q4_0_11008x4096_b4"),
-        (2, 11008, 4096, 8, "q4_0_b8", "Q4_0 GEMV 11008x4096 batch 8", "gemv_q4_0_11008x4096_b8"),
-        (2, 4096, 11008, 4, "q4_0_t_b4", "Q4_0 GEMV 4096x11008 batch 4", "gemv_q4_0_4096x11008_b4"),
-        (2, 4096, 11008, 8, "q4_0_t_b8", "Q4_0 GEMV 4096x11008 batch 8", "gemv_q4_0_4096x11008_b8"),
-        (8, 4096, 4096, 8, "q8_0_b8", "Q8_0 GEMV 4096x4096 batch 8", "gemv_q8_0_4096x4096_b8"),
-        (12, 14336, 4096, 16, "q4_k_b16", "Q4_K GEMV 14336x4096 batch 16", "gemv_q4_k_14336x4096_b16"),
-        (12, 32000, 4096, 16, "q4_k_32000_b16", "Q4_K GEMV 32000x4096 batch 16", "gemv_q4_k_32000x4096_b16"),
-    ]
-    sec = []
-    for qt, M, K, B, label, workload, prof in SECONDARY:
-        steps = max(100, args.steps // (2 if B > 1 or M > 20000 else 1))
-        r = time_gemv(qt, M, K, B, steps, args.warmup, label)
-        log(f"[{label}] {r}")
-        sec.append((workload, prof, r))
-    gv32 = time_gemv_f32(11008, 4096, max(100, args.steps // 4), args.warmup)
-    log(f"[gemv_f32] {gv32}")
-    # read-only streams through the same kernel: the headline's size (1552 x
-    # 4096 f32 = 25.43 MB, the Q4_0 GEMV moves 25.42 MB) and >= 512 MB
-    ro25 = time_gemv_f32(1552, 4096, args.steps, args.warmup)
-    log(f"[read_25mb] {ro25}")
-    ro512 = time_gemv_f32(32768, 4096, max(50, args.steps // 20), max(5, args.warmup // 20))
-    log(f"[read_512mb] {ro512}")
-    sweep = time_gemm_sweep()
-    gsteps = max(5, min(50, args.steps // 40))
-    gemm = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100))
-    log(f"[gemm] {gemm}")
-    gemm_n = time_gemm(4096, 11008, 4096, gsteps, max(2, args.warmup // 100))
-    log(f"[gemm_4096x11008x4096] {gemm_n}")
-    gemm_t = time_gemm(4096, 4096, 4096, gsteps, max(2, args.warmup // 100), transb=True)
-    log(f"[gemm_transb] {gemm_t}")
-    gemm_b = time_gemm_broadcast(8, 1024, 4096, 4096, gsteps, max(2, args.warmup // 100))
-    log(f"[gemm_broadcast] {gemm_b}")
-    cont = time_contiguous((8192, 8192), max(10, args.steps // 20), 5)
-    log(f"[contiguous] {cont}")
-    copy = time_contiguous((8192, 8192), max(10, args.steps // 20), 5, transposed=False)
-    log(f"[copy] {copy}")
-    # one launch moving the headline GEMV's bytes (25,422,848 / 8 elements,
-    # rounded up to whole rows of 1024): what a single launch of that size reaches
-    copy25 = time_copy_like_gemv(3104 * 1024, args.steps, args.warmup)
-    log(f"[copy_25mb] {copy25}")
-    quant = []
-    for qt, label in ((8, "q8_0"), (12, "q4_k")):
-        r = time_quantize(qt, 14336, 4096, max(10, args.steps // (20 if qt == 8 else 100)), 3)
-        log(f"[quantize_{label}] {r}")
-        quant.append((label, r))
-
-    gg = time_gguf_upload(5)
-    log(f"[gguf_upload] {gg}")
-
+    R = run_workloads(KEYS, args.steps, args.warmup)
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     cpu = None if args.no_cpu else cpu_baselines_child(threads)
     if cpu:
         log(f"[cpu] {cpu}")
 
-    def roof_hbm(r, name):
+    def roof_hbm(key):
+        r = R[key]
         achieved = r["alg_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9
         return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(name)}
+                "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(key)}
 
-    def roof_mfma(r, name):
+    def roof_mfma(key):
+        r = R[key]
         achieved = r["flops"] / (r["avg_launch_ms"] * 1e-3) / 1e12
         return {"bound": "mfma", "achieved": achieved, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
-                "frac": achieved / F32_MFMA_PEAK_TFS, "traffic": load_traffic(name)}
+                "frac": achieved / F32_MFMA_PEAK_TFS, "traffic": load_traffic(key)}
 
+    def gemv_line(key, workload, dtype):
+        r = R[key]
+        d = {"workload": workload, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
+             "dtype": dtype, "roofline": roof_hbm(key)}
+        if r.get("launches_per_step", 1) == 2:
+            d["launches_per_step"] = 2
+            d["note"] = ("a step is vx_quantize_x + vx_gemv_xq; roofline.achieved divides the step's algorithmic "
+                         "bytes by vx_gemv_xq's own average duration (graph-replayed alone on a ready split), "
+                         "roofline.traffic is both kernels' HBM bytes per step")
+        return d
+
+    q40 = R["gemv_q4_0_11008x4096_b1"]
+    sweep = R["gemm_sweep"]
+    gg = R["gguf_upload"]
     line = {
         "metric": METRIC,
         "value": q40["value"],
@@ -606,69 +661,53 @@ def main() -> int:
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
                    "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches",
                    "x_repr": X_REPR},
-        "roofline": roof_hbm(q40, "gemv_q4_0_11008x4096_b1"),
+        "roofline": roof_hbm("gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
         "secondary": [
-            {"workload": "Q4_0 GEMV 11008x4096 batch 1, x kept in f32 (VX_GEMV_X_F32: f32 FMA on the exactly "
-                         "decoded weights)", "value": q40f["value"], "unit": "GB/s", "ms_per_step": q40f["ms_per_step"],
-             "dtype": "f32", "roofline": roof_hbm(q40f, "gemv_q4_0_11008x4096_b1_f32x")},
-        ] + [
-            {"workload": wl, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
-             "dtype": DT_INT8X, "roofline": roof_hbm(r, prof)} for wl, prof, r in sec
-        ] + [
-            {"workload": "f32 GEMV y = A x, A 11008x4096 row-major (the GEMM op's N == 1 route, vx_gemv_f32), "
-                         "A rotating over >= 512 MB, HIP-graph replay", "value": gv32["value"], "unit": "GB/s",
-             "ms_per_step": gv32["ms_per_step"], "dtype": "f32", "roofline": roof_hbm(gv32, "gemv_f32_11008x4096")},
-            {"workload": "read-only HBM stream of the headline's size: vx_gemv_f32 on A 1552x4096 f32 (25.43 MB "
-                         "read per launch; the Q4_0 GEMV reads 25.42 MB), A rotating over >= 512 MB, HIP-graph "
-                         "replay (the achievable read rate of one launch this size)", "value": ro25["value"],
-             "unit": "GB/s", "ms_per_step": ro25["ms_per_step"], "dtype": "f32",
-             "roofline": roof_hbm(ro25, "gemv_f32_1552x4096")},
-            {"workload": "read-only HBM stream, 537 MB per launch: vx_gemv_f32 on A 32768x4096 f32 (the achievable "
-                         "read rate of a long stream)", "value": ro512["value"], "unit": "GB/s",
-             "ms_per_step": ro512["ms_per_step"], "dtype": "f32", "roofline": roof_hbm(ro512, "gemv_f32_32768x4096")},
-        ] + [
+            gemv_line("gemv_q4_0_11008x4096_b1_f32x", "Q4_0 GEMV 11008x4096 batch 1, x kept in f32 (VX_GEMV_X_F32: "
+                      "f32 FMA on the exactly decoded weights)", "f32"),
+        ] + [gemv_line(k, v[4], DT_INT8X) for k, v in GEMV_SECONDARY.items()] + [
+            gemv_line("gemv_f32_11008x4096", "f32 GEMV y = A x, A 11008x4096 row-major (the GEMM op's N == 1 route, "
+                      "vx_gemv_f32), A rotating over >= 512 MB, HIP-graph replay", "f32"),
+            gemv_line("gemv_f32_1552x4096", "read-only HBM stream of the headline's size: vx_gemv_f32 on A 1552x4096 "
+                      "f32 (25.43 MB read per launch; the Q4_0 GEMV reads 25.42 MB), A rotating over >= 512 MB, "
+                      "HIP-graph replay (the achievable read rate of one launch this size)", "f32"),
+            gemv_line("gemv_f32_32768x4096", "read-only HBM stream, 537 MB per launch: vx_gemv_f32 on A 32768x4096 "
+                      "f32 (the achievable read rate of a long stream)", "f32"),
             {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
-             "value": cont["value"], "unit": "GB/s", "ms_per_step": cont["ms_per_step"],
-             "roofline": roof_hbm(cont, "contiguous_t8192")},
+             "value": R["contiguous_t8192"]["value"], "unit": "GB/s",
+             "ms_per_step": R["contiguous_t8192"]["ms_per_step"], "roofline": roof_hbm("contiguous_t8192")},
             {"workload": "streaming copy: Contiguous::launch of a contiguous 8192x8192 f32 view (achievable HBM "
                          "bandwidth of a plain read + write stream on this GPU)",
-             "value": copy["value"], "unit": "GB/s", "ms_per_step": copy["ms_per_step"],
-             "roofline": roof_hbm(copy, "copy_8192")},
+             "value": R["copy_8192"]["value"], "unit": "GB/s", "ms_per_step": R["copy_8192"]["ms_per_step"],
+             "roofline": roof_hbm("copy_8192")},
             {"workload": "streaming copy of the headline's size: Contiguous::launch of a contiguous 3104x1024 f32 "
                          "view, 25.43 MB read + written per launch (the headline GEMV moves 25.42 MB), sources "
                          "rotating over >= 512 MB, HIP-graph replay (the achievable rate of one launch this size)",
-             "value": copy25["value"], "unit": "GB/s", "ms_per_step": copy25["ms_per_step"],
-             "roofline": roof_hbm(copy25, "copy_3104x1024")},
+             "value": R["copy_3104x1024"]["value"], "unit": "GB/s", "ms_per_step": R["copy_3104x1024"]["ms_per_step"],
+             "roofline": roof_hbm("copy_3104x1024")},
         ] + [
-            {"workload": f"quantize f32 14336x4096 to {label.upper()} blocks (ggml reference quantizer)",
-             "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
-             "roofline": roof_hbm(r, f"quantize_{label}_14336x4096"),
+            {"workload": f"quantize f32 14336x4096 to {label} blocks (ggml reference quantizer)",
+             "value": R[k]["value"], "unit": "GB/s", "ms_per_step": R[k]["ms_per_step"], "roofline": roof_hbm(k),
              **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block"}
-                if label == "q4_k" else {})}
-            for label, r in quant
+                if label == "Q4_K" else {})}
+            for k, label in (("quantize_q8_0_14336x4096", "Q8_0"), ("quantize_q4_k_14336x4096", "Q4_K"))
         ] + [
             {"workload": "GGUF file (page cache) -> HBM upload, 1.14 GB data section (vx_gguf_upload)",
              "value": gg["value"], "unit": "GB/s", "ms_per_step": gg["ms_per_step"], "open_ms": gg["open_ms"],
              "roofline": {"bound": "pcie", "achieved": gg["value"], "peak": PCIE_PEAK_GBS, "unit": "GB/s",
                           "frac": gg["value"] / PCIE_PEAK_GBS, "traffic": None}},
         ] + [
-            {"workload": "f32 GEMM 4096^3 (row-major A, B)", "value": gemm["value"], "unit": "TFLOP/s",
-             "ms_per_step": gemm["ms_per_step"],
-             "roofline": roof_mfma(gemm, "gemm_f32_4096"),
-             "cpu_baseline": cpu["gemm4096"] if cpu else None,
-             "cpu_baseline_1024": cpu["gemm1024"] if cpu else None},
-            {"workload": "f32 GEMM M=4096 N=11008 K=4096 (row-major A, B)", "value": gemm_n["value"],
-             "unit": "TFLOP/s", "ms_per_step": gemm_n["ms_per_step"],
-             "roofline": roof_mfma(gemm_n, "gemm_f32_4096x11008x4096"),
-             "cpu_baseline": cpu["gemm4096x11008"] if cpu else None},
-            {"workload": "f32 GEMM 4096^3, B a transposed view of a row-major [N, K] buffer", "value": gemm_t["value"],
-             "unit": "TFLOP/s", "ms_per_step": gemm_t["ms_per_step"],
-             "roofline": roof_mfma(gemm_t, "gemm_f32_4096_transb")},
+            {"workload": v[4], "value": R[k]["value"], "unit": "TFLOP/s", "ms_per_step": R[k]["ms_per_step"],
+             "roofline": roof_mfma(k),
+             **({"cpu_baseline": cpu["gemm4096"], "cpu_baseline_1024": cpu["gemm1024"]} if cpu and k == "gemm_f32_4096"
+                else {"cpu_baseline": cpu["gemm4096x11008"]} if cpu and k == "gemm_f32_4096x11008x4096" else {})}
+            for k, v in GEMMS.items()
+        ] + [
             {"workload": "broadcast f32 GEMM out[b] = A[b] W + out[b], A [8, 1024, 4096], shared W [4096, 4096] "
-                         "(vx_gemm_f32_ex, beta = 1)", "value": gemm_b["value"], "unit": "TFLOP/s",
-             "ms_per_step": gemm_b["ms_per_step"],
-             "roofline": roof_mfma(gemm_b, "gemm_f32_broadcast_8x1024")},
+                         "(vx_gemm_f32_ex, beta = 1)", "value": R["gemm_f32_broadcast_8x1024"]["value"],
+             "unit": "TFLOP/s", "ms_per_step": R["gemm_f32_broadcast_8x1024"]["ms_per_step"],
+             "roofline": roof_mfma("gemm_f32_broadcast_8x1024")},
             {"workload": "f32 GEMM sweep of the reference's benchmark (examples/gemm_bench.rs: dim^3 for dim in "
                          "64..4096, 3 warmup + 10 timed launches each), default tiled route and naive kernel",
              "unit": "TFLOP/s", "value": sweep[-1]["tiled_tflops"], "points": sweep},
