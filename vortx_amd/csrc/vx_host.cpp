@@ -15,6 +15,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <algorithm>
 #include <cmath>
 #include <string>
 #include <vector>
@@ -387,22 +388,28 @@ static int run_gemm(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_
     const int am = operand_mode(p.l, 3, 2, p.nb, p.nc);
     const int bm = operand_mode(p.r, 2, 3, p.nb, p.nc);
     int k;
-    // Tile shape: each shape's tiles spread over the CUs, a CU taking
-    // ceil(tiles / CUs) of them; balance = (tiles / CUs) / that. The 64 x 64
-    // kernel reaches ~0.9 of the 128-row kernels' rate on large shapes
-    // (4096^3: 119 vs 131 TFLOP/s) but fills the GPU where those leave CUs
-    // idle (1024^3: 75 vs 28, 3072^3: 108 vs 98.5). 128 x 256 tiles are
-    // taken when they balance clearly better than 128 x 128. All give the
-    // same bits; VX_GEMM_TILE_* (vx_gemm_f32_ex) force one.
+    // Tile shape. 128 x 256 tiles (two resident workgroups per CU) instead of
+    // 128 x 128 (three) when they fill the last round of resident workgroups
+    // clearly better: 4096^3 is 1024 narrow tiles, 1.33 rounds of 768, but 512
+    // wide ones, one round (B transposed 131 -> 137 TFLOP/s). 64 x 64 tiles
+    // when they spread over the CUs better than either, a CU taking
+    // ceil(tiles / CUs) of them, balance = (tiles / CUs) / that, the small
+    // kernel weighted 0.9 for its lower rate on large shapes (4096^3: 119 vs
+    // 131 TFLOP/s): 1024^3 28 -> 75, 1536^3 65 -> 80, 3072^3 96 -> 109. All
+    // give the same bits; VX_GEMM_TILE_* (vx_gemm_f32_ex) force one.
     bool wide = false, small = false;
     if (am == 0 && (bm == 0 || bm == 1)) {
+        const uint64_t tn = (uint64_t)a.tiles_m * a.tiles_n * batch;
+        const uint64_t tw = (uint64_t)a.tiles_m * ((p.N + 255) / 256) * batch;
+        const uint64_t ts = (uint64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch;
+        const uint64_t sn = 3ull * (uint64_t)ctx->num_cus, sw = 2ull * (uint64_t)ctx->num_cus;
+        const double en = (double)tn / (double)(((tn + sn - 1) / sn) * sn);
+        const double ew = (double)tw / (double)(((tw + sw - 1) / sw) * sw);
+        wide = ew > en + 0.05;
         const double cus = (double)ctx->num_cus;
         auto balance = [&](uint64_t t) { return ((double)t / cus) / std::ceil((double)t / cus); };
-        const double bn_ = balance((uint64_t)a.tiles_m * a.tiles_n * batch);
-        const double bw = balance((uint64_t)a.tiles_m * ((p.N + 255) / 256) * batch);
-        const double bs = 0.9 * balance((uint64_t)((p.M + 63) / 64) * ((p.N + 63) / 64) * batch);
-        small = bs > bn_ && bs > bw;
-        wide = !small && bw > bn_ + 0.05;
+        small = 0.9 * balance(ts) > std::max(balance(tn), balance(tw));
+        if (small) wide = false;
         const uint32_t tf = opts ? opts->flags : 0u;
         if (tf & (VX_GEMM_TILE_NARROW | VX_GEMM_TILE_WIDE | VX_GEMM_TILE_SMALL)) {
             wide = (tf & VX_GEMM_TILE_WIDE) != 0;
