@@ -135,10 +135,14 @@ __device__ __forceinline__ void vx_load_frag_full(vx_frag<MODE, TX>& f, const fl
             f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
         }
     } else if constexpr (MODE == MODE_XC) {
+        // the stage's offset k0 * sk is uniform (scalar); the per-thread part
+        // is the same every stage, so the compiler keeps it out of the loop
+        // (written as one product, it cost a 64-bit multiply per load and stage)
+        const float* stage = base + (int64_t)k0 * sk;
 #pragma unroll
         for (int i = 0; i < TX / 64; ++i) {
             const uint32_t fi = t + 256u * i;
-            const f32x4 q = *(const f32x4*)(base + (int64_t)(k0 + fi / QX) * sk + x0 + 4u * (fi % QX));
+            const f32x4 q = *(const f32x4*)(stage + ((int64_t)(fi / QX) * sk + x0 + 4u * (fi % QX)));
             f.v[4 * i + 0] = q.x; f.v[4 * i + 1] = q.y; f.v[4 * i + 2] = q.z; f.v[4 * i + 3] = q.w;
         }
     } else {
