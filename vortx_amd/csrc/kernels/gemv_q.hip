@@ -1103,14 +1103,18 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     float2* scl = (float2*)(red + RMAX * TILE_F) + wave * NSW;   // this wave's [8 XI][CP]
 
     auto row_of = [&](uint32_t ts) { return min((cu + ts * G) * 16u + n, a.M - 1u); };
-    // W loads of tile-work w (clamped to the last one), item j of this wave
-    // (clamped inside the matrix)
+    // W loads of tile-work w, item j of this wave (clamped inside the
+    // matrix). Past the wave's last tile-work every lane loads the first unit
+    // of the matrix: one cache line, where repeating the last item would add
+    // a whole item of L2 reads per ring slot (the loads stay, so the waits
+    // stay exact).
     auto wload = [&](uint32_t w, int j, uint32_t (&r)[NW]) {
+        const bool past = w >= nwork;  // wave-uniform
         w = min(w, nwork - 1u);
         const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
         const uint32_t item = min(p * PI + slot + 16u * (uint32_t)j, ipr - 1u);
-        const uint8_t* rp = a.w + (uint64_t)row_of(ts) * a.row_stride;
-        vx_load_unit<QT, true>(rp, min(4u * item + g, a.nunits - 1u), r);
+        const uint8_t* rp = past ? a.w : a.w + (uint64_t)row_of(ts) * a.row_stride;
+        vx_load_unit<QT, true>(rp, past ? 0u : min(4u * item + g, a.nunits - 1u), r);
     };
     // this wave's x levels and scales of pass p, from clamped addresses.
     // Nothing here uses the loaded values (lanes of columns >= B or of blocks
