@@ -1079,7 +1079,7 @@ __device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
 // (several passes, K past 16 XI items) adds loads of the next pass's x and of
 // y, which makes those waits conservative; it is compiled separately.
 #define VX_XQ_RED_BYTES 65536u
-template <int QT, int NCG, int XI, int RD, bool MP>
+template <int QT, int NCG, int XI, int RD, bool MP, bool ST>
 __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t CP = 8u * NCG;             // columns per launch (padded)
@@ -1112,7 +1112,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         const bool past = w >= nwork;  // wave-uniform
         w = min(w, nwork - 1u);
         const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
-        const uint32_t item = min(p * PI + slot + 16u * (uint32_t)j, ipr - 1u);
+        const uint32_t item = min(p * PI + (uint32_t)XI * slot + (uint32_t)j, ipr - 1u);
         const uint8_t* rp = past ? a.w : a.w + (uint64_t)row_of(ts) * a.row_stride;
         vx_load_unit<QT, true>(rp, past ? 0u : min(4u * item + g, a.nunits - 1u), r);
     };
@@ -1125,16 +1125,16 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     auto pass_loads = [&](uint32_t p) {
 #pragma unroll
         for (int i = 0; i < SPL; ++i) {
-            // entry e = (j, b, col): block 8 (p PI + slot + 16 j) + b
+            // entry e = (j, b, col): block 8 (p PI + XI slot + j) + b
             const uint32_t e = lane + 64u * (uint32_t)i;
             const uint32_t jb = e / CP, col = e - jb * CP;
-            const uint32_t blk = 8u * (p * PI + slot + 16u * (jb >> 3)) + (jb & 7u);
+            const uint32_t blk = 8u * (p * PI + (uint32_t)XI * slot + (jb >> 3)) + (jb & 7u);
             sv[i] = *(const float2*)(a.scales + 2u * ((uint64_t)min(blk, nblk - 1u) * a.xcols + a.col0 +
                                                       min(col, B - 1u)));
         }
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
-            const uint32_t item = p * PI + slot + 16u * (uint32_t)j;
+            const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
 #pragma unroll
             for (int h = 0; h < NCG; ++h) {
                 // lane (i, g): level i % 2 of column 8 h + i / 2, the 8 bytes
@@ -1157,7 +1157,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         for (int i = 0; i < SPL; ++i) {
             const uint32_t e = lane + 64u * (uint32_t)i;
             const uint32_t jb = e / CP, col = e - jb * CP;
-            const uint32_t blk = 8u * (p * PI + slot + 16u * (jb >> 3)) + (jb & 7u);
+            const uint32_t blk = 8u * (p * PI + (uint32_t)XI * slot + (jb >> 3)) + (jb & 7u);
             float2 v = (blk < nblk && col < B) ? sv[i] : float2{0.f, 0.f};
             if constexpr (QT == VX_Q4_0) v.y *= -8.f;
             if (e < NSW) scl[e] = v;
@@ -1171,9 +1171,13 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     pass_publish(0u);
     uint32_t raw[RD * XI][NW];
 #pragma unroll
-    for (int u = 0; u < RD; ++u)
+    for (int u = 0; u < RD; ++u) {
 #pragma unroll
         for (int j = 0; j < XI; ++j) wload((uint32_t)u, j, raw[u * XI + j]);
+        // slots issue in ring order (the scheduler would otherwise reorder
+        // them, and waiting for slot 0 could mean waiting for all of them)
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     float acc[NCG][2];
 #pragma unroll
@@ -1209,7 +1213,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     };
 
     uint32_t wflush = 0;  // first tile-work not yet written to y
-    auto tile_work = [&](uint32_t w, int u) {
+    auto tile_work = [&](uint32_t w, int u, bool refill) {
         const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
         if constexpr (MP) {
             if (ts == 0u && p > 0u) {
@@ -1221,7 +1225,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         (void)ts;
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
-            const uint32_t item = p * PI + slot + 16u * (uint32_t)j;
+            const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
             uint32_t (&rw)[NW] = raw[u * XI + j];
             if (item < ipr) {
                 vx_xq_item<QT> it;
@@ -1264,8 +1268,8 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 }
             }
             // refill this ring slot with the same item of the tile-work RD
-            // ahead (clamped: past the end the last one again, from cache)
-            wload(w + RD, j, rw);
+            // ahead (past the end: one cache line, see wload)
+            if (refill) wload(w + RD, j, rw);
         }
         // park this slot's partial sums; the workgroup reduces every RMAX
         float* rb = red + (w % RMAX) * TILE_F;
@@ -1281,38 +1285,53 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
             wflush = w + 1u;
         }
     };
+    if constexpr (ST) {
+        // (_st kernels: the host takes them when every CU's tile-works fit
+        // the ring) the whole work is in the ring already: straight-line, no
+        // refills. Through the loop below the compiler copies the ring
+        // registers at the loop entry and so waits for the whole ring before
+        // the first tile-work; here each tile-work waits for its own slot.
+#pragma unroll
+        for (int u = 0; u < RD; ++u)
+            if ((uint32_t)u < nwork) tile_work((uint32_t)u, u, false);
+        return;
+    }
     // whole rounds of RD tile-works (every path issues the same loads), then
     // the last partial round
     const uint32_t nfull = nwork - nwork % RD;
     for (uint32_t w0 = 0; w0 < nfull; w0 += RD) {
 #pragma unroll
-        for (int u = 0; u < RD; ++u) tile_work(w0 + (uint32_t)u, u);
+        for (int u = 0; u < RD; ++u) tile_work(w0 + (uint32_t)u, u, true);
     }
 #pragma unroll
     for (int u = 0; u < RD - 1; ++u)
-        if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u);
+        if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u, true);
 }
 
-#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, SFX)                                                   \
+#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, SFX)                                               \
     extern "C" __global__ __launch_bounds__(VX_XQ_WG) void vx_gemv_xq_##QN##_c##NCG##_x##XI##SFX(vx_gemv_xq_args a) { \
-        vx_gemv_xq<QT, NCG, XI, RD, MP>(a);                                                             \
+        vx_gemv_xq<QT, NCG, XI, RD, MP, ST>(a);                                                         \
     }
 // (column groups NCG, items per wave and pass XI, ring depth RD in tiles):
 // RD * XI weight items in flight per wave, as many as the registers allow.
-// One pass (K <= 4096 XI): exact waits; _mp: several passes.
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 1, 4, false, )
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 2, 1, false, )
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, false, )
-VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 3, false, )
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, _mp)
-VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, _mp)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 1, 2, false, )
-VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, false, )
-VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 2, false, )
-VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, _mp)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, _mp)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 1, 3, false, )
-VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, false, )
-VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 2, false, )
-VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, _mp)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, _mp)
+// One pass (K <= 4096 XI): exact waits; _mp: several passes; _st: one pass
+// with at most RD tile-works per wave (no loop).
+#define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                 \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, )      \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, _st)
+VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 1, 4)
+VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
+VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 3, 1)
+VX_GEMV_XQ1(VX_Q4_0, q4_0, 2, 1, 3)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, _mp)
+VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 1, 2)
+VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 2, 1)
+VX_GEMV_XQ1(VX_Q8_0, q8_0, 2, 1, 2)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, _mp)
+VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 1, 3)
+VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 2, 1)
+VX_GEMV_XQ1(VX_Q4_K, q4_k, 2, 1, 2)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, _mp)

@@ -588,21 +588,34 @@ static int run_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* q, const vx
 // Batched GEMV kernel on split x: column groups ncg (1: B <= 8, 2: B <= 16),
 // items per wave and pass xi, one pass or several (mp; K past 16 xi items).
 // The multi-pass kernels use the largest xi of their format.
-static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp) {
+// Ring depth (tile-works in flight per wave) of each one-pass xq kernel, as
+// instantiated in gemv_q.hip.
+static int xq_ring(uint32_t qt, int ncg, int xi) {
+    switch (q_index(qt)) {
+    case 0: return ncg == 2 ? 3 : xi == 1 ? 4 : 1;
+    case 1: return ncg == 2 ? 2 : xi == 1 ? 2 : 1;
+    default: return ncg == 2 ? 2 : xi == 1 ? 3 : 1;
+    }
+}
+
+// st: the straight-line kernel (one pass, every CU's tile-works within the ring)
+static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st) {
+#define VX_XQK(N) (st ? K_vx_gemv_xq_##N##_st : K_vx_gemv_xq_##N)
     switch (q_index(qt)) {
     case 0:
-        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_0_c2_x1_mp : K_vx_gemv_xq_q4_0_c2_x1;
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_0_c2_x1_mp : VX_XQK(q4_0_c2_x1);
         if (mp) return K_vx_gemv_xq_q4_0_c1_x3_mp;
-        return xi == 1 ? K_vx_gemv_xq_q4_0_c1_x1 : xi == 2 ? K_vx_gemv_xq_q4_0_c1_x2 : K_vx_gemv_xq_q4_0_c1_x3;
+        return xi == 1 ? VX_XQK(q4_0_c1_x1) : xi == 2 ? VX_XQK(q4_0_c1_x2) : VX_XQK(q4_0_c1_x3);
     case 1:
-        if (ncg == 2) return mp ? K_vx_gemv_xq_q8_0_c2_x1_mp : K_vx_gemv_xq_q8_0_c2_x1;
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q8_0_c2_x1_mp : VX_XQK(q8_0_c2_x1);
         if (mp) return K_vx_gemv_xq_q8_0_c1_x2_mp;
-        return xi == 1 ? K_vx_gemv_xq_q8_0_c1_x1 : K_vx_gemv_xq_q8_0_c1_x2;
+        return xi == 1 ? VX_XQK(q8_0_c1_x1) : VX_XQK(q8_0_c1_x2);
     default:
-        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_k_c2_x1_mp : K_vx_gemv_xq_q4_k_c2_x1;
+        if (ncg == 2) return mp ? K_vx_gemv_xq_q4_k_c2_x1_mp : VX_XQK(q4_k_c2_x1);
         if (mp) return K_vx_gemv_xq_q4_k_c1_x2_mp;
-        return xi == 1 ? K_vx_gemv_xq_q4_k_c1_x1 : K_vx_gemv_xq_q4_k_c1_x2;
+        return xi == 1 ? VX_XQK(q4_k_c1_x1) : VX_XQK(q4_k_c1_x2);
     }
+#undef VX_XQK
 }
 
 // y [.., M, B] (canonical) = W x, x given by its split q (q->K == K, q->B == B).
@@ -637,8 +650,10 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
         a.npass = (a.ipr + 16u * (uint32_t)xi - 1u) / (16u * (uint32_t)xi);
         // 64 KB of parked partial sums + each of the 16 waves' scales
         const size_t lds = 65536u + (size_t)16u * 8u * (uint32_t)xi * 8u * (uint32_t)ncg * 8u;
-        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream,
-                       a);
+        // every CU's tile-works (at most ceil(tiles / CUs)) fit the ring
+        const uint32_t ntiles = (M + 15u) / 16u, G = (uint32_t)ctx->num_cus;
+        const bool st = !mp && (ntiles + G - 1u) / G <= (uint32_t)xq_ring(w->qtype, ncg, xi);
+        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st), dim3(G), dim3(1024u), lds, stream, a);
         if (s) return s;
     }
     return VX_OK;
