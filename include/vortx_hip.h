@@ -207,13 +207,16 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
  * one f32 scale (|error| <= ~1.6e-5 of the block's max|x|), the products
  * with the weights are exact int32 and the scaling and accumulation are
  * f32. vx_gemv_q_ex(..., VX_GEMV_X_F32) keeps x in f32.
- * With B >= 2 (fast layouts) x is split by vx_quantize_x into a workspace
- * the context owns (allocated on first use and grown when a call needs more;
- * growing synchronizes the device), then vx_gemv_q_xq runs: calls of
- * one context must therefore not overlap in time on different streams, and
- * the first call of a given size must not be made during stream capture
- * (VX_ERR_UNSUPPORTED then). Callers that cannot allocate use
- * vx_gemv_q_noalloc or vx_quantize_x + vx_gemv_q_xq on buffers of their own. */
+ * With 2 <= B <= 8, K <= 4096 and x of stride 1 along K with 16-byte
+ * aligned columns, the batched kernels split x themselves (one launch, no
+ * workspace). Otherwise, with B >= 2 (fast layouts), x is split by
+ * vx_quantize_x into a workspace the context owns (allocated on first use
+ * and grown when a call needs more; growing synchronizes the device), then
+ * vx_gemv_q_xq runs: calls of one context must therefore not overlap in time
+ * on different streams, and the first call of a given size must not be made
+ * during stream capture (VX_ERR_UNSUPPORTED then). Both give the same bits.
+ * Callers that cannot allocate use vx_gemv_q_noalloc or vx_quantize_x +
+ * vx_gemv_q_xq on buffers of their own. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 

@@ -187,3 +187,53 @@ def test_xq_errors(qgemv):
         qgemv.dispatch_xq(torch.empty((B, M), device=DEV).t(), w96, q96)
     with pytest.raises(vx.VortxError, match="VX_ERR_INVALID"):  # buffer too small
         vx.XQ(torch.empty(vx.xq_size(K, B) - 1, dtype=torch.uint8, device=DEV), K, B)
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("M,K,B", [(300, 4096, 8), (131, 4096, 2), (257, 832, 5), (64, 1536, 16), (45, 8192, 3),
+                                   (70, 11008, 4), (33, 4096, 13), (100, 2048, 21), (16, 4096, 9)])
+def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
+    """vx_gemv_q with x stored [B, K] (stride 1 along K) splits x inside the
+    GEMV kernels (one launch); stored [K, B] it runs vx_quantize_x, then the
+    GEMV on the split. Same bytes of x, same kernels otherwise: y is equal bit
+    for bit. (The host fuses only one item and one group of 8 columns per
+    wave, B <= 8 with K <= 4096; the other shapes check that both storages
+    take the split path and agree.)"""
+    if K % O.QTYPE_INFO[qtype][0]:
+        pytest.skip("K not a multiple of the block size")
+    note(f"fused split {QN[qtype]} {M}x{K} B={B}")
+    w = vx.QWeight(S.quant_weights(qtype, M, K, seed=M + K, device=DEV), qtype, M, K)
+    x = S.activations(B, K, seed=B + 1, device=DEV)
+    x[:, :32] = 0.0
+    x[0, 32:64] *= 2.0 ** -110
+    x[-1, 64:96] *= 1e25
+    xkb = x.t().contiguous()  # [K, B] storage: stride B along K
+    y1 = torch.full((B, M), float("nan"), device=DEV)
+    y2 = torch.full((B, M), float("nan"), device=DEV)
+    qgemv.dispatch(y1.t(), w, x.t())
+    qgemv.dispatch(y2.t(), w, xkb)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    ref = O.gemv_q_f64(qtype, w.data.cpu().numpy(), M, K, x.cpu().numpy())
+    assert_close(y1.cpu().numpy().T, ref, tol=2e-4, what=f"fused {QN[qtype]} {M}x{K} b{B}")
+
+
+def test_fused_split_non_finite_column(qgemv):
+    """A NaN / inf in x reaches every y of its column on the fused path too,
+    and only that column, the same way the split path does."""
+    M, K, B = 200, 4096, 6
+    note("fused split non-finite")
+    w = vx.QWeight(S.quant_weights(vx.VX_Q4_0, M, K, seed=3, device=DEV), vx.VX_Q4_0, M, K)
+    x = S.activations(B, K, seed=4, device=DEV)
+    x[1, 100] = float("nan")
+    x[4, 3000] = float("inf")
+    y1 = torch.empty((B, M), device=DEV)
+    y2 = torch.empty((B, M), device=DEV)
+    qgemv.dispatch(y1.t(), w, x.t())
+    qgemv.dispatch(y2.t(), w, x.t().contiguous())
+    torch.cuda.synchronize()
+    fin = torch.isfinite(y1)
+    assert not fin[1].any() and not fin[4].any()
+    assert fin[[0, 2, 3, 5]].all()
+    assert torch.equal(torch.isfinite(y2), fin)
+    assert torch.equal(y1[[0, 2, 3, 5]].view(torch.int32), y2[[0, 2, 3, 5]].view(torch.int32))

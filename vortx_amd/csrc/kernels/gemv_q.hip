@@ -17,6 +17,7 @@
 // from LDS per 8-weight group; lanes are split into 64/LPR row groups so
 // that NB * chunk fits the LDS budget.
 #include "vx_quant.hpp"
+#include "vx_xq.hpp"
 
 extern __shared__ f32x4 vx_lds_x[];
 
@@ -1079,7 +1080,33 @@ __device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
 // (several passes, K past 16 XI items) adds loads of the next pass's x and of
 // y, which makes those waits conservative; it is compiled separately.
 #define VX_XQ_RED_BYTES 65536u
-template <int QT, int NCG, int XI, int RD, bool MP, bool ST>
+// Per wave, after the scales: the fused split's tables ([64] {m, S}, then
+// [64] {c1, i1, i2, fin}), 1536 bytes.
+#define VX_XQ_FX_FLOAT2 192u
+// The two values of v in the 16-lane rows r and r ^ 1 (r ^ 2 for 32), one in
+// each output: a commutative op of the two is the same in every lane.
+__device__ __forceinline__ float vx_pair16_max(float v) {
+    uint32_t a = __float_as_uint(v), b = a;
+    vx_swap16(a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+__device__ __forceinline__ float vx_pair32_max(float v) {
+    uint32_t a = __float_as_uint(v), b = a;
+    vx_swap32(a, b);
+    return fmaxf(__uint_as_float(a), __uint_as_float(b));
+}
+__device__ __forceinline__ float vx_pair16_sum(float v) {
+    uint32_t a = __float_as_uint(v), b = a;
+    vx_swap16(a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+__device__ __forceinline__ float vx_pair32_sum(float v) {
+    uint32_t a = __float_as_uint(v), b = a;
+    vx_swap32(a, b);
+    return __uint_as_float(a) + __uint_as_float(b);
+}
+
+template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX>
 __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t CP = 8u * NCG;             // columns per launch (padded)
@@ -1101,6 +1128,8 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 
     float* red = (float*)vx_lds_x;                               // [RMAX][16][CP][16]
     float2* scl = (float2*)(red + RMAX * TILE_F) + wave * NSW;   // this wave's [8 XI][CP]
+    float2* fxt = (float2*)(red + RMAX * TILE_F) + 16u * NSW + wave * VX_XQ_FX_FLOAT2;  // FX: {m, S}
+    float4* fxp = (float4*)(fxt + 64);                                                  // FX: {c1, i1, i2, fin}
 
     auto row_of = [&](uint32_t ts) { return min((cu + ts * G) * 16u + n, a.M - 1u); };
     // W loads of tile-work w, item j of this wave (clamped inside the
@@ -1166,9 +1195,87 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         __builtin_amdgcn_wave_barrier();
     };
 
-    pass_loads(0u);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    pass_publish(0u);
+    // FX: split this wave's slice of x itself (the bytes vx_quantize_x
+    // writes, from the same arithmetic, vx_xq.hpp), one (item, column group)
+    // at a time. Lane (i, g) holds column 8 h + i / 2 and level L = i % 2 of
+    // the MFMA's A operand: positions 8g..8g+7 of each block, i.e. elements
+    // 4g..4g+3 and 16+4g..16+4g+3. It loads elements 16 L + 4g..+3 (the two
+    // lanes of a column share the loads), so the 32 values of a (block,
+    // column) sit in 8 lanes (L, g), four each: max and sum over g (rows,
+    // swaps of 16 and 32) and L (adjacent lanes, DPP), the sum in the tree of
+    // vx_quantize_x (pairs within each 4; then 4g, 4(g^1); then g, g^2; then
+    // the halves). The scale divisions are spread one (block, column) per
+    // lane through LDS, the levels are formed per lane and the two lanes of
+    // a column swap the halves they need.
+    auto pass_split = [&](uint32_t p) {
+        const uint32_t c8 = n >> 1, L = n & 1u;
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
+#pragma unroll
+            for (int h = 0; h < NCG; ++h) {
+                const uint32_t col = 8u * (uint32_t)h + c8;
+                const float* xp = a.x + (int64_t)(a.col0 + min(col, B - 1u)) * a.xs_b + 16u * L + 4u * g;
+                f32x4 v[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    v[b] = *(const f32x4*)(xp + 32 * (int64_t)min(8u * item + (uint32_t)b, nblk - 1u));
+                float m[8], S[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    float am = fmaxf(fmaxf(fabsf(v[b].x), fabsf(v[b].y)), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
+                    am = vx_pair32_max(vx_pair16_max(am));
+                    m[b] = fmaxf(am, vx_dpp<0xB1>(am));
+                    float s4 = (v[b].x + v[b].y) + (v[b].z + v[b].w);
+                    s4 = vx_pair32_sum(vx_pair16_sum(s4));
+                    S[b] = s4 + vx_dpp<0xB1>(s4);
+                }
+                __builtin_amdgcn_wave_barrier();  // the previous chunk's table reads are done
+                if (L == 0u && g == 0u) {
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) fxt[8u * (uint32_t)b + c8] = float2{m[b], S[b]};
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                __builtin_amdgcn_wave_barrier();
+                {
+                    // lane = (block b2, column c2) of this chunk
+                    const float2 ms = fxt[lane];
+                    const vx_xq_scale sc = vx_xq_scales(ms.x, ms.y);
+                    fxp[lane] = float4{sc.c1, sc.i1, sc.i2, sc.fin ? 1.f : 0.f};
+                    const uint32_t b2 = lane >> 3, c2 = lane & 7u;
+                    const uint32_t blk = 8u * item + b2, colo = 8u * (uint32_t)h + c2;
+                    float2 sv2 = (blk < nblk && colo < B) ? float2{sc.fin ? sc.c2 : ms.x + ms.y, ms.y}
+                                                           : float2{0.f, 0.f};
+                    if constexpr (QT == VX_Q4_0) sv2.y *= -8.f;
+                    scl[(8u * (uint32_t)j + b2) * CP + colo] = sv2;
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const float4 q = fxp[8u * (uint32_t)b + c8];
+                    uint32_t w1, w2;
+                    vx_xq_levels4(v[b], q.x, q.y, q.z, q.w != 0.f, w1, w2);
+                    // level L of positions 8g..8g+3 (L = 0's elements) and
+                    // 8g+4..8g+7 (L = 1's): each lane sends the other level
+                    const uint32_t mine = L ? w2 : w1;
+                    const uint32_t other = __float_as_uint(vx_dpp<0xB1>(__uint_as_float(L ? w1 : w2)));
+                    const uint64_t lo = L ? other : mine, hi = L ? mine : other;
+                    xa[j][b][h] = (long)(lo | (hi << 32));
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    if constexpr (FX) {
+        pass_split(0u);
+    } else {
+        pass_loads(0u);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        pass_publish(0u);
+    }
     uint32_t raw[RD * XI][NW];
 #pragma unroll
     for (int u = 0; u < RD; ++u) {
@@ -1217,9 +1324,13 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         const uint32_t p = MP ? w / nts : 0u, ts = MP ? w - p * nts : w;
         if constexpr (MP) {
             if (ts == 0u && p > 0u) {
-                pass_loads(p);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                pass_publish(p);
+                if constexpr (FX) {
+                    pass_split(p);
+                } else {
+                    pass_loads(p);
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    pass_publish(p);
+                }
             }
         }
         (void)ts;
@@ -1308,30 +1419,33 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u, true);
 }
 
-#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, SFX)                                               \
+#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, FX, SFX)                                           \
     extern "C" __global__ __launch_bounds__(VX_XQ_WG) void vx_gemv_xq_##QN##_c##NCG##_x##XI##SFX(vx_gemv_xq_args a) { \
-        vx_gemv_xq<QT, NCG, XI, RD, MP, ST>(a);                                                         \
+        vx_gemv_xq<QT, NCG, XI, RD, MP, ST, FX>(a);                                                     \
     }
 // (column groups NCG, items per wave and pass XI, ring depth RD in tiles):
 // RD * XI weight items in flight per wave, as many as the registers allow.
 // One pass (K <= 4096 XI): exact waits; _mp: several passes; _st: one pass
-// with at most RD tile-works per wave (no loop).
-#define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                 \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, )      \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, _st)
+// with at most RD tile-works per wave (no loop); _fx: x split in the kernel
+// (x f32 with stride 1 along K) instead of read from a vx_quantize_x split.
+#define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                       \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, false, )     \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st)   \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, true, _fx)   \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, true, _st_fx)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 1, 4)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 3, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 2, 1, 3)
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, _mp)
-VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, false, _mp)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 1, 2)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 2, 1, 2)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, _mp)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, false, _mp)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 1, 3)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 2, 1, 2)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, _mp)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, false, _mp)

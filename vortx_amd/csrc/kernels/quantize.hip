@@ -46,6 +46,7 @@
 
 #include "../vx_kargs.h"
 #include "vx_dpp.hpp"
+#include "vx_xq.hpp"
 
 #pragma clang fp contract(off)
 
@@ -421,8 +422,6 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args
 // Eight lanes per (j, b), lane t holding elements 4t..4t+3; every operation
 // is one IEEE rounding (no contraction in this file), so the bytes equal
 // the oracle's sequential restatement (orc_quantize_x).
-#define VX_XQ_MAGIC 12582912.0f  // 1.5 * 2^23
-
 extern "C" __global__ __launch_bounds__(256) void vx_quantize_x(vx_xq_args a) {
     const uint64_t gid = (uint64_t)blockIdx.x * 256u + threadIdx.x;
     const uint64_t grp = gid >> 3;               // (j, b) = (grp / B, grp % B)
@@ -443,22 +442,11 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_x(vx_xq_args a) {
     }
     const float m = vx_max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     const float S = vx_sum8((v.x + v.y) + (v.z + v.w));
-    const bool fin = m < __builtin_inff() && S == S;
-    const float c1 = m / 126.0f, c2 = c1 / 254.0f;
-    const float i1 = (fin && m >= 0x1p-100f) ? 126.0f / m : 0.0f, i2 = i1 * 254.0f;
-    uint32_t w1 = 0, w2 = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float t1 = fin ? __builtin_fmaf(v[e], i1, VX_XQ_MAGIC) : VX_XQ_MAGIC;
-        t1 = fminf(fmaxf(t1, VX_XQ_MAGIC - 127.0f), VX_XQ_MAGIC + 127.0f);
-        const float q1 = t1 - VX_XQ_MAGIC;  // exact
-        const float r = __builtin_fmaf(-q1, c1, v[e]);
-        float t2 = fin ? __builtin_fmaf(r, i2, VX_XQ_MAGIC) : VX_XQ_MAGIC;
-        t2 = fminf(fmaxf(t2, VX_XQ_MAGIC - 127.0f), VX_XQ_MAGIC + 127.0f);
-        // the low byte of MAGIC + n is n mod 256: the int8 of n
-        w1 |= (__float_as_uint(t1) & 0xFFu) << (8 * e);
-        w2 |= (__float_as_uint(t2) & 0xFFu) << (8 * e);
-    }
+    const vx_xq_scale sc = vx_xq_scales(m, S);
+    const bool fin = sc.fin;
+    const float c2 = sc.c2;
+    uint32_t w1, w2;
+    vx_xq_levels4(v, sc.c1, sc.i1, sc.i2, fin, w1, w2);
     if (in) {
         // position dword dw (positions 4 dw..4 dw + 3, elements 4t..4t+3) of
         // level L sits at ((item B + b) 2 + L) 256 + (dw / 2) 64 + (j % 8) 8 + (dw % 2) 4

@@ -598,9 +598,12 @@ static int xq_ring(uint32_t qt, int ncg, int xi) {
     }
 }
 
-// st: the straight-line kernel (one pass, every CU's tile-works within the ring)
-static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st) {
-#define VX_XQK(N) (st ? K_vx_gemv_xq_##N##_st : K_vx_gemv_xq_##N)
+// st: the straight-line kernel (one pass, every CU's tile-works within the
+// ring); fx: the kernel that splits x itself (one pass only)
+static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx) {
+#define VX_XQK(N)                                                                            \
+    (fx ? (st ? K_vx_gemv_xq_##N##_st_fx : K_vx_gemv_xq_##N##_fx) : (st ? K_vx_gemv_xq_##N##_st \
+                                                                       : K_vx_gemv_xq_##N))
     switch (q_index(qt)) {
     case 0:
         if (ncg == 2) return mp ? K_vx_gemv_xq_q4_0_c2_x1_mp : VX_XQK(q4_0_c2_x1);
@@ -618,15 +621,36 @@ static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st) {
 #undef VX_XQK
 }
 
-// y [.., M, B] (canonical) = W x, x given by its split q (q->K == K, q->B == B).
+// Items per wave and pass for a launch of b columns: the x levels of XI items
+// stay in registers (Q8_0's larger weight items leave room for two, Q4_K's
+// header for two). Sets *mp when K needs several passes.
+static int xq_items(uint32_t qt, uint32_t K, uint32_t b, bool* mp) {
+    const uint32_t ipr = (K / 64u + 3u) / 4u;
+    const int ximax = qt == VX_Q4_0 ? 3 : 2;
+    const int xmax = b > 8u ? 1 : ximax;
+    int xi = (int)((ipr + 15u) / 16u);
+    *mp = xi > xmax;
+    return *mp ? xmax : xi;
+}
+
+// y [.., M, B] (canonical) = W x, x given by its split q (q->K == K, q->B ==
+// B), or, with q == nullptr, split inside the kernels from x itself (cx:
+// stride 1 along K, 16-byte aligned columns; one pass, see xq_fused_ok).
 // Launches of up to 16 columns; W is streamed once per launch.
-static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const vx_qweight* w, const vx_xq* q) {
-    const uint32_t M = w->rows, K = w->cols, B = q->B;
+static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const vx_qweight* w, const vx_xq* q,
+                          const Canon* cx = nullptr, uint32_t Bx = 0) {
+    const uint32_t M = w->rows, K = w->cols, B = q ? q->B : Bx;
+    const bool fx = q == nullptr;
     vx_gemv_xq_args a{};
     a.w = (const uint8_t*)w->base;
     a.row_stride = w->row_stride_bytes;
-    a.levels = (const int8_t*)q->base;
-    a.scales = (const float*)((const uint8_t*)q->base + xq_levels_bytes(K, B));
+    if (fx) {
+        a.x = (const float*)cx->ptr;
+        a.xs_b = cx->l.stride[3];
+    } else {
+        a.levels = (const int8_t*)q->base;
+        a.scales = (const float*)((const uint8_t*)q->base + xq_levels_bytes(K, B));
+    }
     a.ys_m = cy.l.stride[2];
     a.ys_b = cy.l.stride[3];
     a.M = M;
@@ -635,28 +659,39 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
     a.nunits = K / 64u;
     a.ipr = (a.nunits + 3u) / 4u;
     a.xcols = B;
-    // items per wave and pass: x levels of XI items stay in registers (Q8_0's
-    // larger weight items leave room for two, Q4_K's header for two)
-    const int ximax = w->qtype == VX_Q4_0 ? 3 : 2;
     for (uint32_t b0 = 0; b0 < B; b0 += 16u) {
         a.B = B - b0 < 16u ? B - b0 : 16u;
         a.col0 = b0;
         a.y = (float*)(cy.ptr + 4ull * (uint64_t)b0 * (uint64_t)cy.l.stride[3]);
         const int ncg = a.B > 8u ? 2 : 1;
-        const int xmax = ncg == 2 ? 1 : ximax;
-        int xi = (int)((a.ipr + 15u) / 16u);
-        const bool mp = xi > xmax;
-        if (mp) xi = xmax;
+        bool mp;
+        const int xi = xq_items(w->qtype, K, a.B, &mp);
+        if (fx && mp) return fail(VX_ERR_UNSUPPORTED, "internal: the fused split needs one pass");
         a.npass = (a.ipr + 16u * (uint32_t)xi - 1u) / (16u * (uint32_t)xi);
-        // 64 KB of parked partial sums + each of the 16 waves' scales
-        const size_t lds = 65536u + (size_t)16u * 8u * (uint32_t)xi * 8u * (uint32_t)ncg * 8u;
+        // 64 KB of parked partial sums + each of the 16 waves' scales (+ the
+        // fused split's per-wave tables)
+        const size_t lds = 65536u + (size_t)16u * 8u * (uint32_t)xi * 8u * (uint32_t)ncg * 8u + (fx ? 16u * 1536u : 0u);
         // every CU's tile-works (at most ceil(tiles / CUs)) fit the ring
         const uint32_t ntiles = (M + 15u) / 16u, G = (uint32_t)ctx->num_cus;
         const bool st = !mp && (ntiles + G - 1u) / G <= (uint32_t)xq_ring(w->qtype, ncg, xi);
-        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st), dim3(G), dim3(1024u), lds, stream, a);
+        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st, fx), dim3(G), dim3(1024u), lds, stream, a);
         if (s) return s;
     }
     return VX_OK;
+}
+
+// The batched GEMV splits x inside its kernels (one launch, no workspace)
+// when x has stride 1 along K with 16-byte aligned columns and each wave
+// splits one chunk (one item, one group of 8 columns: B <= 8, K <= 4096).
+// Each further chunk adds its own load latency and arithmetic before the
+// weight stream starts, which costs more than the second launch saves
+// (measured: Q4_0 11008x4096 B = 8 13.0 -> 11.7 us per step, but 4096x11008
+// B = 8 (3 items) 15.8 -> 19.9 us and Q4_K 14336x4096 B = 16 (2 column
+// groups) 18.3 -> 21.0 us).
+static bool xq_fused_ok(const vx_qweight* w, const Canon& cx, uint32_t B) {
+    if (B > 8u || cx.l.stride[2] != 1 || !aligned16(cx.ptr) || (B > 1u && cx.l.stride[3] % 4 != 0)) return false;
+    bool mp;
+    return xq_items(w->qtype, w->cols, B, &mp) == 1 && !mp;
 }
 
 static bool xq_layout_ok(const vx_qweight* w) {
@@ -767,6 +802,11 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     // x as two int8 levels per 32-block (the default) or exact f32 (VX_GEMV_X_F32)
     const bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
     const bool force_simt = x_f32;
+    if (B >= 2 && !force_simt && xq_layout_ok(w) && xq_fused_ok(w, cx, B)) {
+        // the matrix-core GEMV splitting x itself: one launch per 16 columns,
+        // W streamed once per launch, no workspace
+        return launch_gemv_xq(ctx, stream, cy, w, nullptr, &cx, B);
+    }
     if (B >= 2 && !force_simt && xq_layout_ok(w)) {
         // split x once into the context's workspace, then the matrix-core
         // GEMV on the split (W streamed once per 16 columns)

@@ -117,6 +117,8 @@ typedef struct vx_gemv_xq_args {
     uint32_t xcols;        /* columns of the split x (its layout pitch) */
     uint32_t col0;         /* first split-x column of this launch (y is already offset) */
     uint32_t pad0;
+    const float* x;        /* kernels that split x themselves (_fx): x[k, b] at x[k + b*xs_b] */
+    int64_t xs_b;
 } vx_gemv_xq_args;
 
 /* Bytes of the device scratch array of vx_gemv_q_noalloc (vx_scratch in
