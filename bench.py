@@ -136,7 +136,11 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     alg = gemv_bytes(qtype, M, K, B)
     r = {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
          "avg_launch_ms": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
-    if B >= 2 and not x_f32:
+    # the library splits x inside the GEMV kernels (one launch) for 2 <= B <= 8
+    # with K <= 4096 and x of stride 1 along K (as here); otherwise a step is
+    # vx_quantize_x + vx_gemv_xq
+    fused = 2 <= B <= 8 and K <= 4096
+    if B >= 2 and not x_f32 and not fused:
         q = vx.XQ.empty(K, B)
         g.quantize_x(q, xv)
         for i in range(min(warmup, 20)):
@@ -639,6 +643,8 @@ def main() -> int:
             d["note"] = ("a step is vx_quantize_x + vx_gemv_xq; roofline.achieved divides the step's algorithmic "
                          "bytes by vx_gemv_xq's own average duration (graph-replayed alone on a ready split), "
                          "roofline.traffic is both kernels' HBM bytes per step")
+        elif key in GEMV_SECONDARY and GEMV_SECONDARY[key][3] >= 2:
+            d["note"] = "one launch per step: the batched GEMV kernel splits x itself"
         return d
 
     q40 = R["gemv_q4_0_11008x4096_b1"]
