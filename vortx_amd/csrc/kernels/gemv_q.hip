@@ -1207,7 +1207,8 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     // the halves). The scale divisions are spread one (block, column) per
     // lane through LDS, the levels are formed per lane and the two lanes of
     // a column swap the halves they need.
-    auto pass_split = [&](uint32_t p) {
+    f32x4 xv[XI][NCG][8];
+    auto pass_split_loads = [&](uint32_t p) {
         const uint32_t c8 = n >> 1, L = n & 1u;
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
@@ -1216,10 +1217,20 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
             for (int h = 0; h < NCG; ++h) {
                 const uint32_t col = 8u * (uint32_t)h + c8;
                 const float* xp = a.x + (int64_t)(a.col0 + min(col, B - 1u)) * a.xs_b + 16u * L + 4u * g;
-                f32x4 v[8];
 #pragma unroll
                 for (int b = 0; b < 8; ++b)
-                    v[b] = *(const f32x4*)(xp + 32 * (int64_t)min(8u * item + (uint32_t)b, nblk - 1u));
+                    xv[j][h][b] = *(const f32x4*)(xp + 32 * (int64_t)min(8u * item + (uint32_t)b, nblk - 1u));
+            }
+        }
+    };
+    auto pass_split_math = [&](uint32_t p) {
+        const uint32_t c8 = n >> 1, L = n & 1u;
+#pragma unroll
+        for (int j = 0; j < XI; ++j) {
+            const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
+#pragma unroll
+            for (int h = 0; h < NCG; ++h) {
+                const f32x4 (&v)[8] = xv[j][h];
                 float m[8], S[8];
 #pragma unroll
                 for (int b = 0; b < 8; ++b) {
@@ -1268,22 +1279,33 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     };
+    auto pass_split = [&](uint32_t p) {
+        pass_split_loads(p);
+        pass_split_math(p);
+    };
 
+    uint32_t raw[RD * XI][NW];
+    auto ring_prologue = [&]() {
+#pragma unroll
+        for (int u = 0; u < RD; ++u) {
+#pragma unroll
+            for (int j = 0; j < XI; ++j) wload((uint32_t)u, j, raw[u * XI + j]);
+            // slots issue in ring order (the scheduler would otherwise reorder
+            // them, and waiting for slot 0 could mean waiting for all of them)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     if constexpr (FX) {
+        // (issuing the ring between the x loads and the split arithmetic, to
+        // overlap the two, measured 8-13 % slower: as with x levels, weight
+        // requests ahead of a CU's x requests delay x more than they gain)
         pass_split(0u);
+        ring_prologue();
     } else {
         pass_loads(0u);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         pass_publish(0u);
-    }
-    uint32_t raw[RD * XI][NW];
-#pragma unroll
-    for (int u = 0; u < RD; ++u) {
-#pragma unroll
-        for (int j = 0; j < XI; ++j) wload((uint32_t)u, j, raw[u * XI + j]);
-        // slots issue in ring order (the scheduler would otherwise reorder
-        // them, and waiting for slot 0 could mean waiting for all of them)
-        __builtin_amdgcn_sched_barrier(0);
+        ring_prologue();
     }
 
     float acc[NCG][2];
@@ -1430,21 +1452,25 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 // (x f32 with stride 1 along K) instead of read from a vx_quantize_x split.
 #define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                       \
     VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, false, )     \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st)   \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, true, _fx)   \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, true, _st_fx)
-VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 1, 4)
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st)
+// the fused split only where each wave splits one chunk (one item, one
+// column group): further chunks cost more than the launch they save
+#define VX_GEMV_XQ1F(QT, QN, RD)                               \
+    VX_GEMV_XQ1(QT, QN, 1, 1, RD)                              \
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx)      \
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx)
+VX_GEMV_XQ1F(VX_Q4_0, q4_0, 4)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 3, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 2, 1, 3)
 VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, false, _mp)
 VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, false, _mp)
-VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 1, 2)
+VX_GEMV_XQ1F(VX_Q8_0, q8_0, 2)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 2, 1, 2)
 VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, false, _mp)
 VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, false, _mp)
-VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 1, 3)
+VX_GEMV_XQ1F(VX_Q4_K, q4_k, 3)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 2, 1, 2)
 VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, false, _mp)

@@ -601,9 +601,13 @@ static int xq_ring(uint32_t qt, int ncg, int xi) {
 // st: the straight-line kernel (one pass, every CU's tile-works within the
 // ring); fx: the kernel that splits x itself (one pass only)
 static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx) {
-#define VX_XQK(N)                                                                            \
-    (fx ? (st ? K_vx_gemv_xq_##N##_st_fx : K_vx_gemv_xq_##N##_fx) : (st ? K_vx_gemv_xq_##N##_st \
-                                                                       : K_vx_gemv_xq_##N))
+#define VX_XQK(N) (st ? K_vx_gemv_xq_##N##_st : K_vx_gemv_xq_##N)
+    if (fx) {  // one item, one column group (xq_fused_ok)
+        const int q = q_index(qt);
+        if (q == 0) return st ? K_vx_gemv_xq_q4_0_c1_x1_st_fx : K_vx_gemv_xq_q4_0_c1_x1_fx;
+        if (q == 1) return st ? K_vx_gemv_xq_q8_0_c1_x1_st_fx : K_vx_gemv_xq_q8_0_c1_x1_fx;
+        return st ? K_vx_gemv_xq_q4_k_c1_x1_st_fx : K_vx_gemv_xq_q4_k_c1_x1_fx;
+    }
     switch (q_index(qt)) {
     case 0:
         if (ncg == 2) return mp ? K_vx_gemv_xq_q4_0_c2_x1_mp : VX_XQK(q4_0_c2_x1);
@@ -666,7 +670,8 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
         const int ncg = a.B > 8u ? 2 : 1;
         bool mp;
         const int xi = xq_items(w->qtype, K, a.B, &mp);
-        if (fx && mp) return fail(VX_ERR_UNSUPPORTED, "internal: the fused split needs one pass");
+        if (fx && (mp || xi != 1 || ncg != 1))
+            return fail(VX_ERR_UNSUPPORTED, "internal: the fused split needs one pass of one item and <= 8 columns");
         a.npass = (a.ipr + 16u * (uint32_t)xi - 1u) / (16u * (uint32_t)xi);
         // 64 KB of parked partial sums + each of the 16 waves' scales (+ the
         // fused split's per-wave tables)
