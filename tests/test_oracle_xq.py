@@ -151,3 +151,47 @@ def test_strided_input_matches_contiguous():
     scales = np.zeros_like(sc)
     assert O.lib().orc_quantize_x(xt.ctypes.data, 4, 1, 256, 4, levels.ctypes.data, scales.ctypes.data) == 0
     assert np.array_equal(levels, lv) and np.array_equal(scales, sc)
+
+
+def _unclamped_levels(x):
+    """Both levels of every 32-block before any clamp, from the stated
+    roundings (f32 scales, exact products, round to nearest even), with the
+    magnitude |r i2| that the second rounding sees."""
+    v = x.reshape(-1, 32).astype(np.float32)
+    m = np.abs(v).max(1)
+    m = m[m >= np.float32(2.0 ** -100)]
+    v = v[np.abs(v).max(1) >= np.float32(2.0 ** -100)]
+    c1 = (m / np.float32(126.0)).astype(np.float32)
+    i1 = (np.float32(126.0) / m).astype(np.float32)
+    i2 = (i1 * np.float32(254.0)).astype(np.float32)
+    q1 = np.rint(v.astype(np.float64) * i1[:, None].astype(np.float64))  # exact product, ties to even
+    r = (v.astype(np.float64) - q1 * c1[:, None].astype(np.float64)).astype(np.float32)
+    t2 = r.astype(np.float64) * i2[:, None].astype(np.float64)
+    return q1, t2
+
+
+def test_clamps_never_act():
+    """The device split computes no clamp (vx_xq_levels4): |v| <= m with
+    i1 = RN(126 / m) keeps |q1| <= 126, and |r| <= c1 (0.5 + 126 2^-23) with
+    i2 = RN(254 i1) keeps |r i2| <= 127.004, which rounds to |q2| <= 127.
+    Checked on random, heavy-tailed and adversarial blocks (values whose first
+    level sits on a half, blocks whose scale products c1 i1 stray furthest
+    from 1), and the oracle's clamped levels equal the unclamped ones."""
+    rng = np.random.default_rng(17)
+    blocks = [rng.standard_normal((4000, 32)), rng.standard_cauchy((4000, 32)),
+              rng.uniform(-1, 1, (4000, 32)) * 10.0 ** rng.integers(-30, 30, (4000, 1))]
+    # first level on a half: v = (k + 1/2 - tiny) c1 for k up to 125, block max m
+    ms = (rng.uniform(1, 2, 4000) * 2.0 ** rng.integers(-90, 90, 4000)).astype(np.float32)
+    k = rng.integers(-125, 126, (4000, 31)) + rng.choice([-0.5, 0.5], (4000, 31)) * (1 - 1e-7)
+    adv = np.concatenate([ms[:, None], k * (ms[:, None] / 126.0)], 1)
+    blocks.append(adv)
+    x = np.concatenate([b.astype(np.float32) for b in blocks])
+    q1, t2 = _unclamped_levels(x)
+    assert np.abs(q1).max() <= 126
+    assert np.abs(t2).max() <= 127.004, np.abs(t2).max()
+    # the split with its clamps gives exactly the rounded, unclamped levels
+    lv, _ = _split(x[:2000].reshape(1, -1))
+    q1c, t2c = _unclamped_levels(x[:2000])
+    got = lv.reshape(-1, 2, 32)
+    pos = O.XQ_POS
+    assert np.array_equal(got[:, 0, pos], q1c) and np.array_equal(got[:, 1, pos], np.rint(t2c))

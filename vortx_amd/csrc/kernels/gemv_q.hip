@@ -901,7 +901,10 @@ VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
 //       Q8_0  acc += d (c2 T)
 //       Q4_K  acc += (d sc) (c2 T) - (dmin m) S
 // Work split: one workgroup of 16 waves per CU (grid = CU count); CU c owns
-// the 16-row tiles c, c + G, ...; wave w owns the K slice s = (w + c) mod 16:
+// rows [c M / G, (c + 1) M / G) in 16-row tiles, the last one possibly
+// partial (its spare lanes repeat the range's last row, which costs no HBM
+// bytes), so every CU streams the same bytes to within one row; wave w owns
+// the K slice s = (w + c) mod 16:
 // items (256 weights) s, s + 16, ... up to XI per pass. The rotation by c
 // keeps the waves of the chip from reading the same slice of x at the same
 // time. A wave loads its slice's x levels into registers once per pass and
@@ -1083,29 +1086,6 @@ __device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
 // Per wave, after the scales: the fused split's tables ([64] {m, S}, then
 // [64] {c1, i1, i2, fin}), 1536 bytes.
 #define VX_XQ_FX_FLOAT2 192u
-// The two values of v in the 16-lane rows r and r ^ 1 (r ^ 2 for 32), one in
-// each output: a commutative op of the two is the same in every lane.
-__device__ __forceinline__ float vx_pair16_max(float v) {
-    uint32_t a = __float_as_uint(v), b = a;
-    vx_swap16(a, b);
-    return fmaxf(__uint_as_float(a), __uint_as_float(b));
-}
-__device__ __forceinline__ float vx_pair32_max(float v) {
-    uint32_t a = __float_as_uint(v), b = a;
-    vx_swap32(a, b);
-    return fmaxf(__uint_as_float(a), __uint_as_float(b));
-}
-__device__ __forceinline__ float vx_pair16_sum(float v) {
-    uint32_t a = __float_as_uint(v), b = a;
-    vx_swap16(a, b);
-    return __uint_as_float(a) + __uint_as_float(b);
-}
-__device__ __forceinline__ float vx_pair32_sum(float v) {
-    uint32_t a = __float_as_uint(v), b = a;
-    vx_swap32(a, b);
-    return __uint_as_float(a) + __uint_as_float(b);
-}
-
 template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX>
 __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
@@ -1119,8 +1099,10 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t G = gridDim.x, cu = blockIdx.x;
-    const uint32_t ntiles = (a.M + 15u) >> 4;
-    const uint32_t nts = ntiles > cu ? (ntiles - cu + G - 1u) / G : 0u;
+    // this CU's rows [r0, r1): M split into G ranges that differ by at most
+    // one row, taken in 16-row tiles (the last one possibly partial)
+    const uint32_t r0 = (uint32_t)((uint64_t)cu * a.M / G), r1 = (uint32_t)((uint64_t)(cu + 1u) * a.M / G);
+    const uint32_t nts = (r1 - r0 + 15u) >> 4;
     if (nts == 0u) return;  // uniform over the workgroup
     const uint32_t slot = (wave + cu) & 15u;
     const uint32_t B = a.B, nblk = a.nblk, ipr = a.ipr;
@@ -1131,7 +1113,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     float2* fxt = (float2*)(red + RMAX * TILE_F) + 16u * NSW + wave * VX_XQ_FX_FLOAT2;  // FX: {m, S}
     float4* fxp = (float4*)(fxt + 64);                                                  // FX: {c1, i1, i2, fin}
 
-    auto row_of = [&](uint32_t ts) { return min((cu + ts * G) * 16u + n, a.M - 1u); };
+    auto row_of = [&](uint32_t ts) { return min(r0 + ts * 16u + n, r1 - 1u); };
     // W loads of tile-work w, item j of this wave (clamped inside the
     // matrix). Past the wave's last tile-work every lane loads the first unit
     // of the matrix: one cache line, where repeating the last item would add
@@ -1231,20 +1213,36 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #pragma unroll
             for (int h = 0; h < NCG; ++h) {
                 const f32x4 (&v)[8] = xv[j][h];
-                float m[8], S[8];
+                // per block: max |v| and sum over the 8 lanes (L, g) of a
+                // column, both through one exchange per step: the even rows
+                // carry the max, the odd rows the sum. The max runs on the
+                // bits (|v| >= 0 orders as unsigned; a NaN then wins, where
+                // fmaxf would skip it, but a NaN makes the sum NaN and the
+                // block non-finite either way). Afterwards rows 0 and 2 hold
+                // m, rows 1 and 3 hold S (S added as vx_quantize_x adds it).
+                uint32_t ms[8];
 #pragma unroll
                 for (int b = 0; b < 8; ++b) {
-                    float am = fmaxf(fmaxf(fabsf(v[b].x), fabsf(v[b].y)), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
-                    am = vx_pair32_max(vx_pair16_max(am));
-                    m[b] = fmaxf(am, vx_dpp<0xB1>(am));
-                    float s4 = (v[b].x + v[b].y) + (v[b].z + v[b].w);
-                    s4 = vx_pair32_sum(vx_pair16_sum(s4));
-                    S[b] = s4 + vx_dpp<0xB1>(s4);
+                    const float am = fmaxf(fmaxf(fabsf(v[b].x), fabsf(v[b].y)), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
+                    const float s4 = (v[b].x + v[b].y) + (v[b].z + v[b].w);
+                    const bool odd = (g & 1u) != 0u;
+                    // rows r, r ^ 1: x = row (r & 2) of (max, sum), y = row (r & 2) + 1
+                    uint32_t x = __float_as_uint(am), y = __float_as_uint(s4);
+                    vx_swap16(x, y);
+                    uint32_t t = odd ? __float_as_uint(__uint_as_float(x) + __uint_as_float(y)) : max(x, y);
+                    // rows r, r ^ 2
+                    uint32_t x2 = t, y2 = t;
+                    vx_swap32(x2, y2);
+                    t = odd ? __float_as_uint(__uint_as_float(x2) + __uint_as_float(y2)) : max(x2, y2);
+                    // lanes L, L ^ 1
+                    const uint32_t o = __float_as_uint(vx_dpp<0xB1>(__uint_as_float(t)));
+                    ms[b] = odd ? __float_as_uint(__uint_as_float(t) + __uint_as_float(o)) : max(t, o);
                 }
                 __builtin_amdgcn_wave_barrier();  // the previous chunk's table reads are done
-                if (L == 0u && g == 0u) {
+                if (L == 0u && g < 2u) {
+                    // g = 0 writes m, g = 1 writes S
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) fxt[8u * (uint32_t)b + c8] = float2{m[b], S[b]};
+                    for (int b = 0; b < 8; ++b) ((uint32_t*)fxt)[2u * (8u * (uint32_t)b + c8) + g] = ms[b];
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                 __builtin_amdgcn_wave_barrier();
@@ -1325,8 +1323,8 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
             const uint32_t k = e / per, rem = e - k * per;
             const uint32_t col = rem >> 4, rr = rem & 15u;
             const uint32_t ts = (w0 + k) % nts;
-            const uint32_t row = (cu + ts * G) * 16u + rr;
-            float* yp = a.y + (int64_t)min(row, a.M - 1u) * a.ys_m + (int64_t)col * a.ys_b;
+            const uint32_t row = r0 + ts * 16u + rr;
+            float* yp = a.y + (int64_t)min(row, r1 - 1u) * a.ys_m + (int64_t)col * a.ys_b;
             float tot = 0.f;
             for (uint32_t w = w0 + k; w <= w1; w += nts) {
                 const float* rb = red + (w % RMAX) * TILE_F;
@@ -1334,9 +1332,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) s += rb[((uint32_t)q * CP + col) * 16u + rr];
                 const uint32_t p = MP ? w / nts : 0u;
-                tot = (w == w0 + k) ? ((MP && p > 0u && row < a.M) ? *yp + s : s) : tot + s;
+                tot = (w == w0 + k) ? ((MP && p > 0u && row < r1) ? *yp + s : s) : tot + s;
             }
-            if (row < a.M) *yp = tot;
+            if (row < r1) *yp = tot;
         }
         __syncthreads();
     };
