@@ -191,7 +191,8 @@ def test_xq_errors(qgemv):
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 @pytest.mark.parametrize("M,K,B", [(300, 4096, 8), (131, 4096, 2), (257, 832, 5), (64, 1536, 16), (45, 8192, 3),
-                                   (70, 11008, 4), (33, 4096, 13), (100, 2048, 21), (16, 4096, 9)])
+                                   (70, 11008, 4), (33, 4096, 13), (100, 2048, 21), (16, 4096, 9),
+                                   (300, 4096, 4), (257, 832, 3), (40, 2048, 4)])
 def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
     """vx_gemv_q with x stored [B, K] (stride 1 along K) splits x inside the
     GEMV kernels (one launch); stored [K, B] it runs vx_quantize_x, then the
@@ -218,22 +219,25 @@ def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
     assert_close(y1.cpu().numpy().T, ref, tol=2e-4, what=f"fused {QN[qtype]} {M}x{K} b{B}")
 
 
-def test_fused_split_non_finite_column(qgemv):
+@pytest.mark.parametrize("B,bad", [(6, (1, 4)), (4, (1, 3))])
+def test_fused_split_non_finite_column(qgemv, B, bad):
     """A NaN / inf in x reaches every y of its column on the fused path too,
-    and only that column, the same way the split path does."""
-    M, K, B = 200, 4096, 6
-    note("fused split non-finite")
+    and only that column, the same way the split path does (B <= 4 runs the
+    fused form whose lanes split half the blocks each)."""
+    M, K = 200, 4096
+    note(f"fused split non-finite B={B}")
     w = vx.QWeight(S.quant_weights(vx.VX_Q4_0, M, K, seed=3, device=DEV), vx.VX_Q4_0, M, K)
     x = S.activations(B, K, seed=4, device=DEV)
-    x[1, 100] = float("nan")
-    x[4, 3000] = float("inf")
+    x[bad[0], 100] = float("nan")
+    x[bad[1], 3000] = float("inf")
     y1 = torch.empty((B, M), device=DEV)
     y2 = torch.empty((B, M), device=DEV)
     qgemv.dispatch(y1.t(), w, x.t())
     qgemv.dispatch(y2.t(), w, x.t().contiguous())
     torch.cuda.synchronize()
+    good = [c for c in range(B) if c not in bad]
     fin = torch.isfinite(y1)
-    assert not fin[1].any() and not fin[4].any()
-    assert fin[[0, 2, 3, 5]].all()
+    assert not fin[bad[0]].any() and not fin[bad[1]].any()
+    assert fin[good].all()
     assert torch.equal(torch.isfinite(y2), fin)
-    assert torch.equal(y1[[0, 2, 3, 5]].view(torch.int32), y2[[0, 2, 3, 5]].view(torch.int32))
+    assert torch.equal(y1[good].view(torch.int32), y2[good].view(torch.int32))

@@ -1086,7 +1086,7 @@ __device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
 // Per wave, after the scales: the fused split's tables ([64] {m, S}, then
 // [64] {c1, i1, i2, fin}), 1536 bytes.
 #define VX_XQ_FX_FLOAT2 192u
-template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX>
+template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX, bool FH>
 __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t CP = 8u * NCG;             // columns per launch (padded)
@@ -1189,30 +1189,39 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     // the halves). The scale divisions are spread one (block, column) per
     // lane through LDS, the levels are formed per lane and the two lanes of
     // a column swap the halves they need.
-    f32x4 xv[XI][NCG][8];
+    // FH (B <= 4): the spare half of the lanes splits the other half of
+    // the blocks: lanes of columns 4 + c (c8 = n / 2 >= 4) take blocks 4..7
+    // of column c, so each lane splits 4 blocks instead of 8, and a row
+    // rotation by 8 (DPP row_ror:8) hands blocks 4..7 to the lanes of column
+    // c. The A rows of columns 4..7 then hold other columns' levels: only
+    // outputs of columns < B are written.
+    constexpr int NBL = FH ? 4 : 8;  // blocks per lane
+    f32x4 xv[XI][NCG][NBL];
     auto pass_split_loads = [&](uint32_t p) {
         const uint32_t c8 = n >> 1, L = n & 1u;
+        const uint32_t cl = FH ? (c8 & 3u) : c8, bo = FH ? 4u * (c8 >> 2) : 0u;
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
             const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
 #pragma unroll
             for (int h = 0; h < NCG; ++h) {
-                const uint32_t col = 8u * (uint32_t)h + c8;
+                const uint32_t col = 8u * (uint32_t)h + cl;
                 const float* xp = a.x + (int64_t)(a.col0 + min(col, B - 1u)) * a.xs_b + 16u * L + 4u * g;
 #pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    xv[j][h][b] = *(const f32x4*)(xp + 32 * (int64_t)min(8u * item + (uint32_t)b, nblk - 1u));
+                for (int b = 0; b < NBL; ++b)
+                    xv[j][h][b] = *(const f32x4*)(xp + 32 * (int64_t)min(8u * item + bo + (uint32_t)b, nblk - 1u));
             }
         }
     };
     auto pass_split_math = [&](uint32_t p) {
         const uint32_t c8 = n >> 1, L = n & 1u;
+        const uint32_t cl = FH ? (c8 & 3u) : c8, bo = FH ? 4u * (c8 >> 2) : 0u;
 #pragma unroll
         for (int j = 0; j < XI; ++j) {
             const uint32_t item = p * PI + (uint32_t)XI * slot + (uint32_t)j;
 #pragma unroll
             for (int h = 0; h < NCG; ++h) {
-                const f32x4 (&v)[8] = xv[j][h];
+                const f32x4 (&v)[NBL] = xv[j][h];
                 // per block: max |v| and sum over the 8 lanes (L, g) of a
                 // column, both through one exchange per step: the even rows
                 // carry the max, the odd rows the sum. The max runs on the
@@ -1220,9 +1229,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 // fmaxf would skip it, but a NaN makes the sum NaN and the
                 // block non-finite either way). Afterwards rows 0 and 2 hold
                 // m, rows 1 and 3 hold S (S added as vx_quantize_x adds it).
-                uint32_t ms[8];
+                uint32_t ms[NBL];
 #pragma unroll
-                for (int b = 0; b < 8; ++b) {
+                for (int b = 0; b < NBL; ++b) {
                     const float am = fmaxf(fmaxf(fabsf(v[b].x), fabsf(v[b].y)), fmaxf(fabsf(v[b].z), fabsf(v[b].w)));
                     const float s4 = (v[b].x + v[b].y) + (v[b].z + v[b].w);
                     const bool odd = (g & 1u) != 0u;
@@ -1242,7 +1251,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 if (L == 0u && g < 2u) {
                     // g = 0 writes m, g = 1 writes S
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) ((uint32_t*)fxt)[2u * (8u * (uint32_t)b + c8) + g] = ms[b];
+                    for (int b = 0; b < NBL; ++b) ((uint32_t*)fxt)[2u * (8u * (bo + (uint32_t)b) + cl) + g] = ms[b];
                 }
                 __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                 __builtin_amdgcn_wave_barrier();
@@ -1261,16 +1270,22 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 __builtin_amdgcn_s_waitcnt(0xC07F);
                 __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                for (int b = 0; b < 8; ++b) {
-                    const float4 q = fxp[8u * (uint32_t)b + c8];
+                for (int b = 0; b < NBL; ++b) {
+                    const float4 q = fxp[8u * (bo + (uint32_t)b) + cl];
                     uint32_t w1, w2;
                     vx_xq_levels4(v[b], q.x, q.y, q.z, q.w != 0.f, w1, w2);
                     // level L of positions 8g..8g+3 (L = 0's elements) and
                     // 8g+4..8g+7 (L = 1's): each lane sends the other level
                     const uint32_t mine = L ? w2 : w1;
                     const uint32_t other = __float_as_uint(vx_dpp<0xB1>(__uint_as_float(L ? w1 : w2)));
-                    const uint64_t lo = L ? other : mine, hi = L ? mine : other;
-                    xa[j][b][h] = (long)(lo | (hi << 32));
+                    const uint32_t lo = L ? other : mine, hi = L ? mine : other;
+                    xa[j][b][h] = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                    if constexpr (FH) {
+                        // lane n + 8 of the row split block 4 + b of this lane's column
+                        const uint32_t lo4 = __float_as_uint(vx_dpp<0x128>(__uint_as_float(lo)));
+                        const uint32_t hi4 = __float_as_uint(vx_dpp<0x128>(__uint_as_float(hi)));
+                        xa[j][4 + b][h] = (long)((uint64_t)lo4 | ((uint64_t)hi4 << 32));
+                    }
                 }
             }
         }
@@ -1439,9 +1454,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u, true);
 }
 
-#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, FX, SFX)                                           \
+#define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, FX, SFX, FH)                                       \
     extern "C" __global__ __launch_bounds__(VX_XQ_WG) void vx_gemv_xq_##QN##_c##NCG##_x##XI##SFX(vx_gemv_xq_args a) { \
-        vx_gemv_xq<QT, NCG, XI, RD, MP, ST, FX>(a);                                                     \
+        vx_gemv_xq<QT, NCG, XI, RD, MP, ST, FX, FH>(a);                                                 \
     }
 // (column groups NCG, items per wave and pass XI, ring depth RD in tiles):
 // RD * XI weight items in flight per wave, as many as the registers allow.
@@ -1449,27 +1464,29 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 // with at most RD tile-works per wave (no loop); _fx: x split in the kernel
 // (x f32 with stride 1 along K) instead of read from a vx_quantize_x split.
 #define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                       \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, false, )     \
-    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st)
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, false, , false)     \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st, false)
 // the fused split only where each wave splits one chunk (one item, one
 // column group): further chunks cost more than the launch they save
 #define VX_GEMV_XQ1F(QT, QN, RD)                               \
     VX_GEMV_XQ1(QT, QN, 1, 1, RD)                              \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx)      \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx)
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx, false)      \
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx, false)    \
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx4, true)      \
+    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx4, true)
 VX_GEMV_XQ1F(VX_Q4_0, q4_0, 4)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 3, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 2, 1, 3)
-VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, false, _mp)
-VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, false, _mp, false)
+VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, false, _mp, false)
 VX_GEMV_XQ1F(VX_Q8_0, q8_0, 2)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 2, 1, 2)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, false, _mp)
-VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, false, _mp, false)
+VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, false, _mp, false)
 VX_GEMV_XQ1F(VX_Q4_K, q4_k, 3)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 2, 1)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 2, 1, 2)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, false, _mp)
-VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, false, _mp)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, false, _mp, false)
+VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, false, _mp, false)

@@ -15,6 +15,7 @@
 //   0x140 row_mirror            lane i <- 15 - i  within each 16 lanes
 //   0x142 row_bcast:15          row r <- lane 15 of row r - 1
 //   0x143 row_bcast:31          rows 2, 3 <- lane 31
+//   0x128 row_ror:8             lane i <- (i + 8) mod 16 within each 16 lanes
 // ROWS masks the 16-lane rows that are written; the others (and any lane
 // whose source is invalid) receive 0, so v + vx_dpp(v) leaves them as v.
 template <int CTRL, int ROWS = 0xF>

@@ -599,14 +599,17 @@ static int xq_ring(uint32_t qt, int ncg, int xi) {
 }
 
 // st: the straight-line kernel (one pass, every CU's tile-works within the
-// ring); fx: the kernel that splits x itself (one pass only)
-static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx) {
+// ring); fx: the kernel that splits x itself (one pass only); fh: its form
+// for <= 4 columns, each lane splitting half the blocks
+static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx, bool fh = false) {
 #define VX_XQK(N) (st ? K_vx_gemv_xq_##N##_st : K_vx_gemv_xq_##N)
+#define VX_XQF(N) (fh ? (st ? K_vx_gemv_xq_##N##_st_fx4 : K_vx_gemv_xq_##N##_fx4) \
+                      : (st ? K_vx_gemv_xq_##N##_st_fx : K_vx_gemv_xq_##N##_fx))
     if (fx) {  // one item, one column group (xq_fused_ok)
         const int q = q_index(qt);
-        if (q == 0) return st ? K_vx_gemv_xq_q4_0_c1_x1_st_fx : K_vx_gemv_xq_q4_0_c1_x1_fx;
-        if (q == 1) return st ? K_vx_gemv_xq_q8_0_c1_x1_st_fx : K_vx_gemv_xq_q8_0_c1_x1_fx;
-        return st ? K_vx_gemv_xq_q4_k_c1_x1_st_fx : K_vx_gemv_xq_q4_k_c1_x1_fx;
+        if (q == 0) return VX_XQF(q4_0_c1_x1);
+        if (q == 1) return VX_XQF(q8_0_c1_x1);
+        return VX_XQF(q4_k_c1_x1);
     }
     switch (q_index(qt)) {
     case 0:
@@ -623,6 +626,7 @@ static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx) {
         return xi == 1 ? VX_XQK(q4_k_c1_x1) : VX_XQK(q4_k_c1_x2);
     }
 #undef VX_XQK
+#undef VX_XQF
 }
 
 // Items per wave and pass for a launch of b columns: the x levels of XI items
@@ -679,7 +683,7 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
         // every CU's tile-works (at most ceil(ceil(M / CUs) / 16)) fit the ring
         const uint32_t G = (uint32_t)ctx->num_cus, tmax = ((M + G - 1u) / G + 15u) / 16u;
         const bool st = !mp && tmax <= (uint32_t)xq_ring(w->qtype, ncg, xi);
-        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st, fx), dim3(G), dim3(1024u), lds, stream, a);
+        int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st, fx, a.B <= 4u), dim3(G), dim3(1024u), lds, stream, a);
         if (s) return s;
     }
     return VX_OK;
