@@ -695,7 +695,9 @@ def main() -> int:
         ] + [
             {"workload": f"quantize f32 14336x4096 to {label} blocks (ggml reference quantizer)",
              "value": R[k]["value"], "unit": "GB/s", "ms_per_step": R[k]["ms_per_step"], "roofline": roof_hbm(k),
-             **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block"}
+             **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block, one "
+                         "sub-block per lane, 11-13k VALU instructions per wave (ISA count): 0.53-0.59 ms at one "
+                         "wave-instruction per CU per cycle (256 CUs, 2.4 GHz); the HBM fraction is not its bound"}
                 if label == "Q4_K" else {})}
             for k, label in (("quantize_q8_0_14336x4096", "Q8_0"), ("quantize_q4_k_14336x4096", "Q4_K"))
         ] + [
