@@ -903,8 +903,10 @@ VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
 // Work split: one workgroup of 16 waves per CU (grid = CU count); CU c owns
 // rows [c M / G, (c + 1) M / G) in 16-row tiles, the last one possibly
 // partial (its spare lanes repeat the range's last row, which costs no HBM
-// bytes), so every CU streams the same bytes to within one row; wave w owns
-// the K slice s = (w + c) mod 16:
+// bytes), so every CU streams the same bytes to within one row; with two
+// column groups, where the arithmetic bounds the kernel, CU c owns the whole
+// tiles c, c + G, ... instead (no partial tile's arithmetic on every CU);
+// wave w owns the K slice s = (w + c) mod 16:
 // items (256 weights) s, s + 16, ... up to XI per pass. The rotation by c
 // keeps the waves of the chip from reading the same slice of x at the same
 // time. A wave loads its slice's x levels into registers once per pass and
@@ -1099,10 +1101,26 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
     const uint32_t G = gridDim.x, cu = blockIdx.x;
-    // this CU's rows [r0, r1): M split into G ranges that differ by at most
-    // one row, taken in 16-row tiles (the last one possibly partial)
-    const uint32_t r0 = (uint32_t)((uint64_t)cu * a.M / G), r1 = (uint32_t)((uint64_t)(cu + 1u) * a.M / G);
-    const uint32_t nts = (r1 - r0 + 15u) >> 4;
+    // this CU's tile-work ts covers rows rb + ts rs .. + 15, below rlim:
+    // rows [r0, r1), M split into G ranges that differ by at most one row,
+    // in 16-row tiles (the last one possibly partial), or with two column
+    // groups (WHOLE) the whole tiles cu, cu + G, ...: where the arithmetic,
+    // not the stream, bounds the kernel, that computes fewer row slots
+    constexpr bool WHOLE = NCG == 2;
+    uint32_t rb, rs, rlim, nts;
+    if constexpr (WHOLE) {
+        const uint32_t ntiles = (a.M + 15u) >> 4;
+        rb = 16u * cu;
+        rs = 16u * G;
+        rlim = a.M;
+        nts = ntiles > cu ? (ntiles - cu + G - 1u) / G : 0u;
+    } else {
+        const uint32_t r0 = (uint32_t)((uint64_t)cu * a.M / G), r1 = (uint32_t)((uint64_t)(cu + 1u) * a.M / G);
+        rb = r0;
+        rs = 16u;
+        rlim = r1;
+        nts = (r1 - r0 + 15u) >> 4;
+    }
     if (nts == 0u) return;  // uniform over the workgroup
     const uint32_t slot = (wave + cu) & 15u;
     const uint32_t B = a.B, nblk = a.nblk, ipr = a.ipr;
@@ -1113,7 +1131,7 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     float2* fxt = (float2*)(red + RMAX * TILE_F) + 16u * NSW + wave * VX_XQ_FX_FLOAT2;  // FX: {m, S}
     float4* fxp = (float4*)(fxt + 64);                                                  // FX: {c1, i1, i2, fin}
 
-    auto row_of = [&](uint32_t ts) { return min(r0 + ts * 16u + n, r1 - 1u); };
+    auto row_of = [&](uint32_t ts) { return min(rb + ts * rs + n, rlim - 1u); };
     // W loads of tile-work w, item j of this wave (clamped inside the
     // matrix). Past the wave's last tile-work every lane loads the first unit
     // of the matrix: one cache line, where repeating the last item would add
@@ -1338,8 +1356,8 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
             const uint32_t k = e / per, rem = e - k * per;
             const uint32_t col = rem >> 4, rr = rem & 15u;
             const uint32_t ts = (w0 + k) % nts;
-            const uint32_t row = r0 + ts * 16u + rr;
-            float* yp = a.y + (int64_t)min(row, r1 - 1u) * a.ys_m + (int64_t)col * a.ys_b;
+            const uint32_t row = rb + ts * rs + rr;
+            float* yp = a.y + (int64_t)min(row, rlim - 1u) * a.ys_m + (int64_t)col * a.ys_b;
             float tot = 0.f;
             for (uint32_t w = w0 + k; w <= w1; w += nts) {
                 const float* rb = red + (w % RMAX) * TILE_F;
@@ -1347,9 +1365,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q) s += rb[((uint32_t)q * CP + col) * 16u + rr];
                 const uint32_t p = MP ? w / nts : 0u;
-                tot = (w == w0 + k) ? ((MP && p > 0u && row < r1) ? *yp + s : s) : tot + s;
+                tot = (w == w0 + k) ? ((MP && p > 0u && row < rlim) ? *yp + s : s) : tot + s;
             }
-            if (row < r1) *yp = tot;
+            if (row < rlim) *yp = tot;
         }
         __syncthreads();
     };

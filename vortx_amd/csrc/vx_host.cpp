@@ -680,8 +680,12 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
         // 64 KB of parked partial sums + each of the 16 waves' scales (+ the
         // fused split's per-wave tables)
         const size_t lds = 65536u + (size_t)16u * 8u * (uint32_t)xi * 8u * (uint32_t)ncg * 8u + (fx ? 16u * 1536u : 0u);
-        // every CU's tile-works (at most ceil(ceil(M / CUs) / 16)) fit the ring
-        const uint32_t G = (uint32_t)ctx->num_cus, tmax = ((M + G - 1u) / G + 15u) / 16u;
+        // the kernels' row split: balanced row ranges for one column group,
+        // whole tiles for two (measured: Q4_K 14336x4096 / 32000x4096 B = 16
+        // 0.35 / 0.7 us faster whole, B <= 8 0.1-0.35 us faster balanced);
+        // every CU's tile-works must fit the ring for the _st kernels
+        const uint32_t G = (uint32_t)ctx->num_cus;
+        const uint32_t tmax = ncg == 2 ? ((M + 15u) / 16u + G - 1u) / G : ((M + G - 1u) / G + 15u) / 16u;
         const bool st = !mp && tmax <= (uint32_t)xq_ring(w->qtype, ncg, xi);
         int s = launch(ctx, xq_kernel(w->qtype, ncg, xi, mp, st, fx, a.B <= 4u), dim3(G), dim3(1024u), lds, stream, a);
         if (s) return s;
