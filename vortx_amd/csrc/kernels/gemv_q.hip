@@ -1274,8 +1274,10 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
                 __builtin_amdgcn_wave_barrier();
                 {
-                    // lane = (block b2, column c2) of this chunk
-                    const float2 ms = fxt[lane];
+                    // lane = (block b2, column c2) of this chunk (FH: the
+                    // table holds columns 0..3 only; the others are never
+                    // read back and publish zero scales)
+                    const float2 ms = (FH && (lane & 7u) >= 4u) ? float2{0.f, 0.f} : fxt[lane];
                     const vx_xq_scale sc = vx_xq_scales(ms.x, ms.y);
                     fxp[lane] = float4{sc.c1, sc.i1, sc.i2, sc.fin ? 1.f : 0.f};
                     const uint32_t b2 = lane >> 3, c2 = lane & 7u;
