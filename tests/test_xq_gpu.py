@@ -241,3 +241,39 @@ def test_fused_split_non_finite_column(qgemv, B, bad):
     assert fin[good].all()
     assert torch.equal(torch.isfinite(y2), fin)
     assert torch.equal(y1[good].view(torch.int32), y2[good].view(torch.int32))
+
+
+def _sweep_cases(n=24, seed=2024):
+    rng = np.random.default_rng(seed)
+    cases = []
+    while len(cases) < n:
+        qtype = QTYPES[rng.integers(len(QTYPES))]
+        qk = 256 if qtype == vx.VX_Q4_K else 64
+        K = int(qk * rng.integers(1, 12288 // qk + 1))
+        M = int(rng.choice([rng.integers(1, 40), rng.integers(40, 600), rng.integers(600, 3000)]))
+        B = int(rng.integers(2, 17))
+        if M * K * B <= 40_000_000:
+            cases.append((qtype, M, K, B))
+    return cases
+
+
+_SWEEP = _sweep_cases()
+
+
+@pytest.mark.parametrize("qtype,M,K,B", _SWEEP, ids=[f"{QN[q]}-{m}x{k}-b{b}" for q, m, k, b in _SWEEP])
+def test_batched_random_shapes(qgemv, qtype, M, K, B):
+    """Seeded random shapes across every batched route (fused one-launch
+    kernels, split + GEMV with one or two column groups, one or several
+    passes, partial tiles and items): x stored [B, K] and [K, B] give the same
+    bits, and both stay within the tolerance of the exact f64 product."""
+    note(f"batched sweep {QN[qtype]} {M}x{K} B={B}")
+    w = vx.QWeight(S.quant_weights(qtype, M, K, seed=M * 7 + K, device=DEV), qtype, M, K)
+    x = S.activations(B, K, seed=M + 3 * B, device=DEV)
+    y1 = torch.full((B, M), float("nan"), device=DEV)
+    y2 = torch.full((B, M), float("nan"), device=DEV)
+    qgemv.dispatch(y1.t(), w, x.t())
+    qgemv.dispatch(y2.t(), w, x.t().contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    ref = O.gemv_q_f64(qtype, w.data.cpu().numpy(), M, K, x.cpu().numpy())
+    assert_close(y1.cpu().numpy().T, ref, tol=2e-4, what=f"{QN[qtype]} {M}x{K} b{B}")
