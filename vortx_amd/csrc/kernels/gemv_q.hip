@@ -899,7 +899,8 @@ VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
 //     int32, |D| < 2^20), and applies the block's scales in f32:
 //       Q4_0  acc += d (c2 T - 8 S)       (nibbles used unbiased)
 //       Q8_0  acc += d (c2 T)
-//       Q4_K  acc += (d sc) (c2 T) - (dmin m) S
+//       Q4_K  acc += d (sum over the item's sub-blocks of sc (c2 T))
+//                  - dmin (sum of m S)   (one super-block per item)
 // Work split: one workgroup of 16 waves per CU (grid = CU count); CU c owns
 // rows [c M / G, (c + 1) M / G) in 16-row tiles, the last one possibly
 // partial (its spare lanes repeat the range's last row, which costs no HBM
@@ -967,13 +968,6 @@ struct vx_xq_item {
     float ds[8];            // d of block b, this lane's row (Q4_0, Q8_0)
     uint32_t scm[4];        // Q4_K: sub-blocks 2k, 2k + 1: bytes sc, m, sc, m (6-bit)
     float d, dmin;          // Q4_K super-block scales
-    // Q4_K: d sc and -dmin m of sub-block b
-    __device__ __forceinline__ float dsc(int b) const {
-        return d * (float)((scm[b >> 1] >> (16 * (b & 1))) & 0xFFu);
-    }
-    __device__ __forceinline__ float dmm(int b) const {
-        return -(dmin * (float)((scm[b >> 1] >> (16 * (b & 1) + 8)) & 0xFFu));
-    }
 };
 
 template <int QT>
@@ -1397,6 +1391,10 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                 vx_xq_item<QT> it;
                 vx_xq_prepare<QT>(rw, g, it);
                 const uint32_t bl0 = 8u * (uint32_t)j;  // first block of the item in this wave's scales
+                // Q4_K: the item's sums before its d / dmin (one super-block)
+                float q1s[NCG][2], q2s[NCG][2];
+#pragma unroll
+                for (int h = 0; h < NCG; ++h) q1s[h][0] = q1s[h][1] = q2s[h][0] = q2s[h][1] = 0.f;
                 // block b of the item: MFMA per column group, then the scales
                 auto block = [&](int b) {
                     const long bw = (long)((uint64_t)it.lo[b] | ((uint64_t)it.hi[b] << 32));
@@ -1414,10 +1412,11 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
                             } else if constexpr (QT == VX_Q8_0) {
                                 v = __builtin_fmaf(it.ds[b], c2 * T, v);
                             } else {
-                                v = __builtin_fmaf(it.dsc(b), c2 * T, v);
-                                v = __builtin_fmaf(it.dmm(b), sx, v);
+                                const uint32_t sm = it.scm[b >> 1] >> (16 * (b & 1));
+                                q1s[h][c] = __builtin_fmaf((float)(sm & 0xFFu), c2 * T, q1s[h][c]);
+                                q2s[h][c] = __builtin_fmaf((float)((sm >> 8) & 0xFFu), sx, q2s[h][c]);
                             }
-                            acc[h][c] = v;
+                            if constexpr (QT != VX_Q4_K) acc[h][c] = v;
                         }
                     }
                 };
@@ -1431,6 +1430,13 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #pragma unroll
                     for (int b = 0; b < 8; ++b)
                         if ((uint32_t)b < nb) block(b);
+                }
+                if constexpr (QT == VX_Q4_K) {
+#pragma unroll
+                    for (int h = 0; h < NCG; ++h)
+#pragma unroll
+                        for (int c = 0; c < 2; ++c)
+                            acc[h][c] = __builtin_fmaf(-it.dmin, q2s[h][c], __builtin_fmaf(it.d, q1s[h][c], acc[h][c]));
                 }
             }
             // refill this ring slot with the same item of the tile-work RD
