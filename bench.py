@@ -6,31 +6,29 @@ W 11008 x 4096, batch 1, throughput in GB/s of algorithmic bytes
 next of >= 512 MB of distinct weight copies (so the 256 MB Infinity Cache
 cannot serve them), inputs resident in HBM before timing starts.
 
-Secondary lines in the same JSON object: the other BASELINE GEMV configs
-(Q8_0 4096 x 4096 b=1 and b=8, Q4_K 32000 x 4096 and 14336 x 4096 b=1,
-Q4_0 4096 x 11008 b=1, b=4 and b=8, Q4_0 11008 x 4096 b=4 and b=8, Q4_K
-14336 x 4096 and 32000 x 4096 b=16; GB/s of algorithmic bytes), the f32
-GEMV 11008 x 4096 and the same kernel as a read-only stream at the
-headline's size and at 537 MB, the contiguous copy of a transposed
-8192^2 view and a plain streaming copy of a contiguous one (the achievable
-bandwidth beside the 8 TB/s peak), the same streaming copy at the headline's
-size (25.4 MB per launch, graph-replayed: the achievable rate of one launch
-that small), the Q8_0 and Q4_K quantizers on 14336 x 4096, the GGUF file
--> HBM upload (against the PCIe 5.0 x16 link) and the f32 GEMMs 4096^3,
-4096 x 11008 x 4096, 4096^3 with a transposed-B view and the broadcast
-batch (TFLOP/s), and the reference's GEMM size sweep (64..4096, tiled and
-naive), each with its roofline, plus CPU baselines from the
-oracle's OpenMP restatements on the host cores.
+Beside it, top-level objects for the metric's other halves and the
+ceiling: Q8_0 4096 x 4096 b=1, the headline with x kept in f32, the read
+probe (the headline GEMV's loads of W alone: the most its access pattern
+can stream in one launch) and the f32 GEMM 4096^3 (TFLOP/s, >= 50 timed
+launches after 10 warmups). Compact lines ([value, ms per step, roofline
+achieved, roofline frac, launches per step]) cover the other BASELINE GEMV
+configs, the activation split kernel alone, the f32 GEMV as a read-only
+stream (headline size, 537 MB), copies (transposed 8192^2 view, contiguous
+8192^2, one launch of the headline's 25.4 MB), the quantizers, the other
+GEMM shapes and the broadcast batch; then the GGUF upload, the reference's
+GEMM size sweep (examples/gemm_bench.rs: 64..4096, tiled and naive) and
+CPU baselines from the oracle's OpenMP restatements on the host cores.
 
 Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
 (captured eager launches) between two synchronizations (wall clock).
-`roofline.achieved` divides the algorithmic bytes (or flops) of one launch
-by the kernel's average launch duration: HIP events recorded on the stream
-the kernels run on, bracketing the same timed region, divided by the number
-of launches. rocprofv3 summaries of the same command are kept under
-profiles/.
+`roofline.achieved` divides the algorithmic bytes (or flops) of one step by
+the step's average duration from HIP events recorded on the stream the
+kernels run on, bracketing the same timed region (a two-launch batched step
+counts both launches; its GEMV kernel alone is reported as `gemv_only`).
+rocprofv3 summaries of the same command are kept under profiles/. Nothing
+goes to stderr without --verbose.
 
-Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
+Usage: python bench.py [--gpus 1] [--steps 2000] [--warmup 200] [--verbose] [--only KEYS]
 """
 from __future__ import annotations
 
@@ -55,8 +53,21 @@ X_REPR = ("x rounded per 32-element block to c (254 x1 + x2), x1 and x2 int8, c 
           "|error| <= c / 2 ~ 1.6e-5 max|x_blk| per element")
 
 
+VERBOSE = False
+
+
 def log(msg: str) -> None:
-    print(msg, file=sys.stderr, flush=True)
+    """Progress on stderr, only with --verbose (the driver keeps the tail of
+    the output, which must hold the whole JSON line)."""
+    if VERBOSE:
+        print(msg, file=sys.stderr, flush=True)
+
+
+def rnd(v, sig: int = 4):
+    """v rounded to `sig` significant digits (compact JSON)."""
+    if v is None or isinstance(v, (bool, int, str)):
+        return v
+    return float(f"{v:.{sig}g}")
 
 
 def gemv_bytes(qtype: int, M: int, K: int, B: int) -> int:
@@ -65,7 +76,8 @@ def gemv_bytes(qtype: int, M: int, K: int, B: int) -> int:
 
 
 def load_traffic(name: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/*.json)."""
+    """HBM bytes per launch (per step for two-launch lines) measured with
+    rocprofv3 --pmc, kept in profiles/traffic_<name>.json."""
     p = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
     if os.path.exists(p):
         with open(p) as f:
@@ -104,43 +116,56 @@ def graph_time(launch, steps: int):
     return reps * chunk, wall, e0.elapsed_time(e1)
 
 
-def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str, x_f32: bool = False):
-    """One step = vx_gemv_q on the next of >= 512 MB of weight copies
-    (K launches captured into a HIP graph and replayed; HIP events on the
-    graph's stream bracket the timed region). At B >= 2 on the default int8-x
-    path a step is two launches (vx_quantize_x, then vx_gemv_xq); the GEMV
-    kernel is then also timed alone, on a ready split, for the roofline."""
+def weight_copies(qtype: int, M: int, K: int, dev):
+    """>= 512 MB of weight copies (twice the 256 MB Infinity Cache), four
+    distinct seeds."""
+    from vortx_amd import synthetic as S
+    nbytes = M * S.row_bytes(qtype, K)
+    ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
+    distinct = [S.quant_weights(qtype, M, K, seed=100 + i, device=dev) for i in range(min(4, ncopy))]
+    return [distinct[i % len(distinct)].clone() for i in range(ncopy)]
+
+
+def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label: str, x_f32: bool = False,
+              probe: bool = False):
+    """One step = vx_gemv_q_ws on the next of >= 512 MB of weight copies
+    (launches captured into a HIP graph and replayed; HIP events on the
+    graph's stream bracket the timed region). At B >= 2 on the int8 path, a
+    shape the GEMV kernel cannot split x for is two launches per step
+    (vx_quantize_x into the caller's workspace, then vx_gemv_xq); the GEMV
+    kernel is then also timed alone on a ready split. probe: the read probe
+    (vx_gemv_q_read_probe) over the same copies instead of the GEMV."""
     import torch
 
     import vortx_amd as vx
     from vortx_amd import synthetic as S
 
     dev = torch.device("cuda:0")
-    nbytes = M * S.row_bytes(qtype, K)
-    ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
-    log(f"[{label}] generating {ncopy} weight copies ({ncopy * nbytes / 2**20:.0f} MiB)")
-    log(f"[copies] {ncopy} x {nbytes}")
-    distinct = [S.quant_weights(qtype, M, K, seed=100 + i, device=dev) for i in range(min(4, ncopy))]
-    ws = [distinct[i % len(distinct)].clone() for i in range(ncopy)]
-    del distinct
+    ws = weight_copies(qtype, M, K, dev)
+    ncopy = len(ws)
+    log(f"[{label}] {ncopy} weight copies of {ws[0].numel()} B")
     x = S.activations(B, K, seed=7, device=dev)
     y = torch.empty((B, M), device=dev)
     g = vx.QuantGemv(0)
     qws = [vx.QWeight(w, qtype, M, K) for w in ws]
     xv, yv = x.t(), y.t()
-
+    wsp = vx.QuantGemv.workspace(qws[0], B)
+    if probe:
+        yp = torch.empty(M, device=dev)
+        fn = lambda i, s=None: g.read_probe(yp, qws[i % ncopy], stream=s)  # noqa: E731
+    else:
+        fn = lambda i, s=None: g.dispatch(yv, qws[i % ncopy], xv, stream=s, x_f32=x_f32, workspace=wsp)  # noqa: E731
     for i in range(warmup):
-        g.dispatch(yv, qws[i % ncopy], xv, x_f32=x_f32)
+        fn(i)
     torch.cuda.synchronize()
-    done, wall, ev_ms = graph_time(lambda i, s: g.dispatch(yv, qws[i % ncopy], xv, stream=s, x_f32=x_f32), steps)
-    alg = gemv_bytes(qtype, M, K, B)
+    done, wall, ev_ms = graph_time(fn, steps)
+    alg = M * S.row_bytes(qtype, K) + 4 * M if probe else gemv_bytes(qtype, M, K, B)
     r = {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
-         "avg_launch_ms": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
-    # the library splits x inside the GEMV kernels (one launch) for 2 <= B <= 8
-    # with K <= 4096 and x of stride 1 along K (as here); otherwise a step is
-    # vx_quantize_x + vx_gemv_xq
+         "step_ms_events": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
+    # the library's own route choice, read back: a fused shape splits x inside
+    # the GEMV (one launch); the others split into the workspace first
     fused = 2 <= B <= 8 and K <= 4096
-    if B >= 2 and not x_f32 and not fused:
+    if B >= 2 and not x_f32 and not probe and not fused:
         q = vx.XQ.empty(K, B)
         g.quantize_x(q, xv)
         for i in range(min(warmup, 20)):
@@ -148,15 +173,14 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
         torch.cuda.synchronize()
         n2, _, ev2 = graph_time(lambda i, s: g.dispatch_xq(yv, qws[i % ncopy], q, stream=s), steps)
         r["launches_per_step"] = 2
-        r["step_ms_events"] = r["avg_launch_ms"]
-        r["avg_launch_ms"] = ev2 / n2  # the dominant kernel (vx_gemv_xq) alone
+        r["gemv_ms_events"] = ev2 / n2  # vx_gemv_xq alone, on a ready split
     return r
 
 
 def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
     """f32 GEMV y = A x (the GEMM op's N == 1 route, vx_gemv_f32): A [M, K]
     row-major f32 read once, so 4 M K + 4 K + 4 M algorithmic bytes per launch;
-    A rotating over >= 512 MB of copies, K launches captured into a HIP graph
+    A rotating over >= 512 MB of copies, launches captured into a HIP graph
     and replayed as in time_gemv. A read-only HBM stream with one FMA per
     element: the achievable read rate of a launch that size."""
     import torch
@@ -166,7 +190,6 @@ def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
     dev = torch.device("cuda:0")
     nbytes = 4 * M * K
     ncopy = max(2, -(-(512 << 20) // nbytes) + 1)
-    log(f"[copies] {ncopy} x {nbytes}")
     base = [torch.randn((M, K), device=dev) for _ in range(min(4, ncopy))]
     As = [base[i % len(base)].clone() if i >= len(base) else base[i] for i in range(ncopy)]
     x = torch.randn((K, 1), device=dev)
@@ -175,31 +198,29 @@ def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
     for i in range(warmup):
         gm.dispatch(y, As[i % ncopy], x)
     torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    chunk = min(steps, 500)
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(chunk):
-                gm.dispatch(y, As[i % ncopy], x, stream=s)
-    torch.cuda.synchronize()
-    reps = max(1, steps // chunk)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
-        graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(s)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(s)
-        torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    done = reps * chunk
+    done, wall, ev = graph_time(lambda i, s: gm.dispatch(y, As[i % ncopy], x, stream=s), steps)
     alg = 4 * M * K + 4 * K + 4 * M
     return {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
-            "avg_launch_ms": e0.elapsed_time(e1) / done, "alg_bytes": alg, "copies": ncopy}
+            "step_ms_events": ev / done, "alg_bytes": alg, "copies": ncopy}
+
+
+def event_time(fn, steps: int, warmup: int):
+    """warmup eager calls, then `steps` timed ones between two
+    synchronizations: (wall seconds, HIP-event ms on the current stream)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, e0.elapsed_time(e1)
 
 
 def time_gemm_sweep(dims=(64, 128, 256, 512, 768, 1024, 1536, 2048, 4096)):
@@ -218,21 +239,10 @@ def time_gemm_sweep(dims=(64, 128, 256, 512, 768, 1024, 1536, 2048, 4096)):
         a = S.uniform((d, d), 1, dev)
         b = S.uniform((d, d), 2, dev)
         c = torch.empty((d, d), device=dev)
-        row = {"dim": d}
-        for name, fn in (("tiled", gm.dispatch), ("naive", gm.dispatch_naive)):
-            for _ in range(3):
-                fn(c, a, b)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(10):
-                fn(c, a, b)
-            e1.record()
-            torch.cuda.synchronize()
-            ms = e0.elapsed_time(e1) / 10
-            row[f"{name}_ms"] = ms
-            row[f"{name}_tflops"] = 2.0 * d ** 3 / (ms * 1e-3) / 1e12
-        row["speedup"] = row["naive_ms"] / row["tiled_ms"]
+        row = [d]
+        for fn in (gm.dispatch, gm.dispatch_naive):
+            _, ev = event_time(lambda: fn(c, a, b), 10, 3)
+            row.append(2.0 * d ** 3 / (ev / 10 * 1e-3) / 1e12)
         pts.append(row)
         log(f"[gemm_sweep] {row}")
     return pts
@@ -251,22 +261,10 @@ def time_gemm(M: int, N: int, K: int, steps: int, warmup: int, transb: bool = Fa
     b = S.uniform((N, K), 2, dev).t() if transb else S.uniform((K, N), 2, dev)
     c = torch.empty((M, N), device=dev)
     gm = vx.Gemm(0)
-    for _ in range(warmup):
-        gm.dispatch(c, a, b)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    stream = torch.cuda.current_stream()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        gm.dispatch(c, a, b)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    launch_ms = e0.elapsed_time(e1) / steps
+    wall, ev = event_time(lambda: gm.dispatch(c, a, b), steps, warmup)
     flops = 2.0 * M * N * K
-    return {"value": flops * steps / wall / 1e12, "avg_launch_ms": launch_ms, "flops": flops,
-            "ms_per_step": wall * 1e3 / steps}
+    return {"value": flops * steps / wall / 1e12, "step_ms_events": ev / steps, "flops": flops,
+            "ms_per_step": wall * 1e3 / steps, "steps": steps}
 
 
 def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int):
@@ -283,27 +281,16 @@ def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int)
     w = S.uniform((K, N), 4, dev)
     c = torch.zeros((B, M, N), device=dev)
     gm = vx.Gemm(0)
-    for _ in range(warmup):
-        gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    stream = torch.cuda.current_stream()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
-        gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    wall, ev = event_time(lambda: gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True), steps, warmup)
     flops = 2.0 * B * M * N * K
-    return {"value": flops * steps / wall / 1e12, "avg_launch_ms": e0.elapsed_time(e1) / steps, "flops": flops,
-            "ms_per_step": wall * 1e3 / steps}
+    return {"value": flops * steps / wall / 1e12, "step_ms_events": ev / steps, "flops": flops,
+            "ms_per_step": wall * 1e3 / steps, "steps": steps}
 
 
 def time_copy_like_gemv(nelem: int, steps: int, warmup: int):
     """The achievable bandwidth of ONE launch as large as the headline GEMV:
     Contiguous::launch of a contiguous f32 view of nelem elements (8 bytes
-    per element, read + write), sources rotating over >= 512 MB, K launches
+    per element, read + write), sources rotating over >= 512 MB, launches
     captured into a HIP graph and replayed exactly as time_gemv does."""
     import torch
 
@@ -313,37 +300,15 @@ def time_copy_like_gemv(nelem: int, steps: int, warmup: int):
     shape = (nelem // 1024, 1024)
     nsrc = -(-(512 << 20) // (4 * nelem)) + 1
     srcs = [torch.randn(shape, device=dev) for _ in range(min(4, nsrc))]
-    log(f"[copies] {nsrc} x {4 * shape[0] * shape[1]}")
     srcs = [srcs[i % len(srcs)].clone() for i in range(nsrc)]
     out = torch.empty(shape, device=dev)
     c = vx.Contiguous(0)
     for i in range(warmup):
         c.launch(out, srcs[i % nsrc])
     torch.cuda.synchronize()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    chunk = min(steps, 500)
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(chunk):
-                c.launch(out, srcs[i % nsrc], stream=s)
-    torch.cuda.synchronize()
-    reps = max(1, steps // chunk)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
-        graph.replay()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        e0.record(s)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(s)
-        torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    done = reps * chunk
+    done, wall, ev = graph_time(lambda i, s: c.launch(out, srcs[i % nsrc], stream=s), steps)
     nbytes = 8 * out.numel()
-    return {"value": nbytes * done / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / done,
+    return {"value": nbytes * done / wall / 1e9, "step_ms_events": ev / done,
             "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / done, "sources": nsrc}
 
 
@@ -362,20 +327,10 @@ def time_contiguous(shape, steps: int, warmup: int, transposed: bool = True):
         srcs = [t.t() for t in srcs]
     out = torch.empty(srcs[0].shape, device=dev)
     c = vx.Contiguous(0)
-    for i in range(warmup):
-        c.launch(out, srcs[i % 4])
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for i in range(steps):
-        c.launch(out, srcs[i % 4])
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    it = iter(range(1 << 30))
+    wall, ev = event_time(lambda: c.launch(out, srcs[next(it) % 4]), steps, warmup)
     nbytes = 8 * out.numel()
-    return {"value": nbytes * steps / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / steps,
+    return {"value": nbytes * steps / wall / 1e9, "step_ms_events": ev / steps,
             "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
 
 
@@ -393,21 +348,33 @@ def time_quantize(qtype: int, M: int, K: int, steps: int, warmup: int):
     buf = torch.empty(M * (K // qk) * bb, dtype=torch.uint8, device=dev)
     w = vx.QWeight(buf, qtype, M, K)
     qg = vx.QuantGemv(0)
-    for i in range(warmup):
-        qg.quantize(w, xs[i % 2])
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for i in range(steps):
-        qg.quantize(w, xs[i % 2])
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    it = iter(range(1 << 30))
+    wall, ev = event_time(lambda: qg.quantize(w, xs[next(it) % 2]), steps, warmup)
     nbytes = 4 * M * K + buf.numel()
-    return {"value": nbytes * steps / wall / 1e9, "avg_launch_ms": e0.elapsed_time(e1) / steps,
+    return {"value": nbytes * steps / wall / 1e9, "step_ms_events": ev / steps,
             "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
+
+
+def time_quantize_x(K: int, B: int, steps: int, warmup: int):
+    """vx_quantize_x alone (the split step of the two-launch batched GEMV):
+    x [K, B] f32 read (4 B K), levels and scales written (vx_xq_size);
+    launches captured into a HIP graph and replayed."""
+    import torch
+
+    import vortx_amd as vx
+    from vortx_amd import synthetic as S
+
+    dev = torch.device("cuda:0")
+    x = S.activations(B, K, seed=7, device=dev)
+    q = vx.XQ.empty(K, B)
+    g = vx.QuantGemv(0)
+    for _ in range(warmup):
+        g.quantize_x(q, x.t())
+    torch.cuda.synchronize()
+    done, wall, ev = graph_time(lambda i, s: g.quantize_x(q, x.t(), stream=s), steps)
+    nbytes = 4 * B * K + vx.xq_size(K, B)
+    return {"value": nbytes * done / wall / 1e9, "step_ms_events": ev / done, "alg_bytes": nbytes,
+            "ms_per_step": wall * 1e3 / done}
 
 
 def time_gguf_upload(steps: int):
@@ -509,73 +476,88 @@ def cpu_baselines_child(threads: int):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
-# Batched and secondary GEMV configs: key -> (qtype, M, K, B, workload).
+# GEMV configs beside the headline: key -> (qtype, M, K, B, workload).
 GEMV_SECONDARY = {
-    "gemv_q8_0_4096x4096_b1": (8, 4096, 4096, 1, "Q8_0 GEMV 4096x4096 batch 1"),
-    "gemv_q4_k_32000x4096_b1": (12, 32000, 4096, 1, "Q4_K GEMV 32000x4096 batch 1"),
-    "gemv_q4_0_4096x11008_b1": (2, 4096, 11008, 1, "Q4_0 GEMV 4096x11008 batch 1"),
-    "gemv_q4_k_14336x4096_b1": (12, 14336, 4096, 1, "Q4_K GEMV 14336x4096 batch 1"),
-    "gemv_q4_0_11008x4096_b4": (2, 11008, 4096, 4, "Q4_0 GEMV 11008x4096 batch 4"),
-    "gemv_q4_0_11008x4096_b8": (2, 11008, 4096, 8, "Q4_0 GEMV 11008x4096 batch 8"),
-    "gemv_q4_0_4096x11008_b4": (2, 4096, 11008, 4, "Q4_0 GEMV 4096x11008 batch 4"),
-    "gemv_q4_0_4096x11008_b8": (2, 4096, 11008, 8, "Q4_0 GEMV 4096x11008 batch 8"),
-    "gemv_q8_0_4096x4096_b8": (8, 4096, 4096, 8, "Q8_0 GEMV 4096x4096 batch 8"),
-    "gemv_q4_k_14336x4096_b16": (12, 14336, 4096, 16, "Q4_K GEMV 14336x4096 batch 16"),
-    "gemv_q4_k_32000x4096_b16": (12, 32000, 4096, 16, "Q4_K GEMV 32000x4096 batch 16"),
+    "gemv_q4_k_32000x4096_b1": (12, 32000, 4096, 1, "Q4_K 32000x4096 b=1"),
+    "gemv_q4_0_4096x11008_b1": (2, 4096, 11008, 1, "Q4_0 4096x11008 b=1"),
+    "gemv_q4_k_14336x4096_b1": (12, 14336, 4096, 1, "Q4_K 14336x4096 b=1"),
+    "gemv_q4_0_11008x4096_b4": (2, 11008, 4096, 4, "Q4_0 11008x4096 b=4"),
+    "gemv_q4_0_11008x4096_b8": (2, 11008, 4096, 8, "Q4_0 11008x4096 b=8"),
+    "gemv_q4_0_4096x11008_b4": (2, 4096, 11008, 4, "Q4_0 4096x11008 b=4"),
+    "gemv_q4_0_4096x11008_b8": (2, 4096, 11008, 8, "Q4_0 4096x11008 b=8"),
+    "gemv_q8_0_4096x4096_b8": (8, 4096, 4096, 8, "Q8_0 4096x4096 b=8"),
+    "gemv_q4_k_14336x4096_b16": (12, 14336, 4096, 16, "Q4_K 14336x4096 b=16"),
+    "gemv_q4_k_32000x4096_b16": (12, 32000, 4096, 16, "Q4_K 32000x4096 b=16"),
 }
 GEMMS = {  # key -> (M, N, K, transb, workload)
-    "gemm_f32_4096": (4096, 4096, 4096, False, "f32 GEMM 4096^3 (row-major A, B)"),
-    "gemm_f32_4096x11008x4096": (4096, 11008, 4096, False, "f32 GEMM M=4096 N=11008 K=4096 (row-major A, B)"),
-    "gemm_f32_4096_transb": (4096, 4096, 4096, True, "f32 GEMM 4096^3, B a transposed view of a row-major [N, K] buffer"),
+    "gemm_f32_4096": (4096, 4096, 4096, False, "f32 GEMM 4096^3, row-major A and B"),
+    "gemm_f32_4096x11008x4096": (4096, 11008, 4096, False, "f32 GEMM M=4096 N=11008 K=4096, row-major"),
+    "gemm_f32_4096_transb": (4096, 4096, 4096, True, "f32 GEMM 4096^3, B a transposed view of an [N,K] buffer"),
 }
 # every workload in run order (the keys --only selects from)
-KEYS = (["gemv_q4_0_11008x4096_b1", "gemv_q4_0_11008x4096_b1_f32x"] + list(GEMV_SECONDARY) +
-        ["gemv_f32_11008x4096", "gemv_f32_1552x4096", "gemv_f32_32768x4096", "gemm_sweep"] + list(GEMMS) +
-        ["gemm_f32_broadcast_8x1024", "contiguous_t8192", "copy_8192", "copy_3104x1024", "quantize_q8_0_14336x4096",
-         "quantize_q4_k_14336x4096", "gguf_upload"])
+KEYS = (["gemv_q4_0_11008x4096_b1", "gemv_q8_0_4096x4096_b1", "gemv_q4_0_11008x4096_b1_f32x",
+         "read_q4_0_11008x4096", "read_q8_0_4096x4096"] + list(GEMV_SECONDARY) +
+        ["split_x_11008_b8", "split_x_4096_b16", "gemv_f32_11008x4096", "gemv_f32_1552x4096",
+         "gemv_f32_32768x4096"] + list(GEMMS) +
+        ["gemm_f32_broadcast_8x1024", "gemm_sweep", "contiguous_t8192", "copy_8192", "copy_3104x1024",
+         "quantize_q8_0_14336x4096", "quantize_q4_k_14336x4096", "gguf_upload"])
+# GEMMs: at least this many timed launches after this many warmups, whatever --steps is
+GEMM_STEPS, GEMM_WARMUP = 50, 10
 
 
 def run_workloads(keys, steps: int, warmup: int) -> dict:
-    """Run the named workloads in KEYS order; returns key -> result."""
+    """Run the named workloads in KEYS order; returns key -> result. The
+    headline takes exactly `steps` timed steps after `warmup`; the other lines
+    take at least 1000 launches (GEMV-sized) or 50 (GEMMs)."""
     out = {}
-    gsteps, gwarm = max(5, min(50, steps // 40)), max(2, warmup // 100)
+    many = max(1000, steps)
     for k in [k for k in KEYS if k in keys]:
         if k == "gemv_q4_0_11008x4096_b1":
-            r = time_gemv(2, 11008, 4096, 1, steps, warmup, "q4_0")
+            r = time_gemv(2, 11008, 4096, 1, steps, warmup, k)
+        elif k == "gemv_q8_0_4096x4096_b1":
+            r = time_gemv(8, 4096, 4096, 1, many, max(warmup, 50), k)
         elif k == "gemv_q4_0_11008x4096_b1_f32x":
             # the headline config with x kept in f32 (VX_GEMV_X_F32): f32 FMA on
             # the exactly decoded weights, the exact-arithmetic twin of the default
-            r = time_gemv(2, 11008, 4096, 1, steps, warmup, "q4_0_f32x", x_f32=True)
+            r = time_gemv(2, 11008, 4096, 1, many, max(warmup, 50), k, x_f32=True)
+        elif k == "read_q4_0_11008x4096":
+            r = time_gemv(2, 11008, 4096, 1, many, max(warmup, 50), k, probe=True)
+        elif k == "read_q8_0_4096x4096":
+            r = time_gemv(8, 4096, 4096, 1, many, max(warmup, 50), k, probe=True)
         elif k in GEMV_SECONDARY:
             qt, M, K, B, _ = GEMV_SECONDARY[k]
-            r = time_gemv(qt, M, K, B, max(100, steps // (2 if B > 1 or M > 20000 else 1)), warmup, k)
+            r = time_gemv(qt, M, K, B, many, max(warmup, 50), k)
+        elif k == "split_x_11008_b8":
+            r = time_quantize_x(11008, 8, many, 50)
+        elif k == "split_x_4096_b16":
+            r = time_quantize_x(4096, 16, many, 50)
         elif k == "gemv_f32_11008x4096":
-            r = time_gemv_f32(11008, 4096, max(100, steps // 4), warmup)
+            r = time_gemv_f32(11008, 4096, many, 50)
         elif k == "gemv_f32_1552x4096":
             # a read-only stream of the headline's size: 1552 x 4096 f32 = 25.43 MB
             # (the Q4_0 GEMV moves 25.42 MB)
-            r = time_gemv_f32(1552, 4096, steps, warmup)
+            r = time_gemv_f32(1552, 4096, many, 50)
         elif k == "gemv_f32_32768x4096":
-            r = time_gemv_f32(32768, 4096, max(50, steps // 20), max(5, warmup // 20))
+            r = time_gemv_f32(32768, 4096, 100, 5)
         elif k == "gemm_sweep":
             r = time_gemm_sweep()
         elif k in GEMMS:
             M, N, K, tb, _ = GEMMS[k]
-            r = time_gemm(M, N, K, gsteps, gwarm, transb=tb)
+            r = time_gemm(M, N, K, GEMM_STEPS, GEMM_WARMUP, transb=tb)
         elif k == "gemm_f32_broadcast_8x1024":
-            r = time_gemm_broadcast(8, 1024, 4096, 4096, gsteps, gwarm)
+            r = time_gemm_broadcast(8, 1024, 4096, 4096, GEMM_STEPS, GEMM_WARMUP)
         elif k == "contiguous_t8192":
-            r = time_contiguous((8192, 8192), max(10, steps // 20), 5)
+            r = time_contiguous((8192, 8192), 100, 5)
         elif k == "copy_8192":
-            r = time_contiguous((8192, 8192), max(10, steps // 20), 5, transposed=False)
+            r = time_contiguous((8192, 8192), 100, 5, transposed=False)
         elif k == "copy_3104x1024":
             # one launch moving the headline GEMV's bytes (25,422,848 / 8 elements,
             # rounded up to whole rows of 1024)
-            r = time_copy_like_gemv(3104 * 1024, steps, warmup)
+            r = time_copy_like_gemv(3104 * 1024, many, 50)
         elif k == "quantize_q8_0_14336x4096":
-            r = time_quantize(8, 14336, 4096, max(10, steps // 20), 3)
+            r = time_quantize(8, 14336, 4096, 100, 3)
         elif k == "quantize_q4_k_14336x4096":
-            r = time_quantize(12, 14336, 4096, max(10, steps // 100), 3)
+            r = time_quantize(12, 14336, 4096, 20, 3)
         else:  # gguf_upload
             r = time_gguf_upload(5)
         log(f"[{k}] {r}")
@@ -583,18 +565,34 @@ def run_workloads(keys, steps: int, warmup: int) -> dict:
     return out
 
 
+def roof(r: dict, key: str, bound: str = "hbm") -> dict:
+    """roofline object of one line: algorithmic bytes (flops) of a step over
+    the step's HIP-event time (both launches of a two-launch step)."""
+    t = r["step_ms_events"] * 1e-3
+    if bound == "hbm":
+        a, peak, unit = r["alg_bytes"] / t / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        a, peak, unit = r["flops"] / t / 1e12, F32_MFMA_PEAK_TFS, "TFLOP/s"
+    tr = load_traffic(key)
+    return {"bound": bound, "achieved": rnd(a), "peak": peak, "unit": unit, "frac": rnd(a / peak, 3),
+            "traffic": int(tr) if tr else None}
+
+
 def main() -> int:
+    global VERBOSE
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--verbose", action="store_true", help="progress lines on stderr")
     ap.add_argument("--only", default="", metavar="KEYS",
                     help="comma-separated workload keys (profiling runs): print their raw results, not the "
                          "benchmark line; keys: " + ", ".join(KEYS))
     ap.add_argument("--cpu-baseline-only", type=int, default=0, metavar="THREADS",
                     help=argparse.SUPPRESS)  # the CPU leg's own process: print its JSON and exit
     args = ap.parse_args()
+    VERBOSE = args.verbose
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the hot path shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -619,45 +617,35 @@ def main() -> int:
     R = run_workloads(KEYS, args.steps, args.warmup)
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     cpu = None if args.no_cpu else cpu_baselines_child(threads)
-    if cpu:
-        log(f"[cpu] {cpu}")
 
-    def roof_hbm(key):
+    def gline(key: str, workload: str, unit: str = "GB/s", bound: str = "hbm") -> dict:
         r = R[key]
-        achieved = r["alg_bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9
-        return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": load_traffic(key)}
-
-    def roof_mfma(key):
-        r = R[key]
-        achieved = r["flops"] / (r["avg_launch_ms"] * 1e-3) / 1e12
-        return {"bound": "mfma", "achieved": achieved, "peak": F32_MFMA_PEAK_TFS, "unit": "TFLOP/s",
-                "frac": achieved / F32_MFMA_PEAK_TFS, "traffic": load_traffic(key)}
-
-    def gemv_line(key, workload, dtype):
-        r = R[key]
-        d = {"workload": workload, "value": r["value"], "unit": "GB/s", "ms_per_step": r["ms_per_step"],
-             "dtype": dtype, "roofline": roof_hbm(key)}
+        d = {"workload": workload, "value": rnd(r["value"]), "unit": unit, "ms_per_step": rnd(r["ms_per_step"]),
+             "roofline": roof(r, key, bound)}
         if r.get("launches_per_step", 1) == 2:
-            d["launches_per_step"] = 2
-            d["note"] = ("a step is vx_quantize_x + vx_gemv_xq; roofline.achieved divides the step's algorithmic "
-                         "bytes by vx_gemv_xq's own average duration (graph-replayed alone on a ready split), "
-                         "roofline.traffic is both kernels' HBM bytes per step")
-        elif key in GEMV_SECONDARY and GEMV_SECONDARY[key][3] >= 2:
-            d["note"] = "one launch per step: the batched GEMV kernel splits x itself"
+            # a two-launch step: the GEMV kernel alone (on a ready split) beside it
+            g = r["gemv_ms_events"]
+            d["launches"] = 2
+            d["gemv_only"] = {"us": rnd(g * 1e3), "GB/s": rnd(r["alg_bytes"] / (g * 1e-3) / 1e9)}
         return d
 
+    def short(key: str, unit: str = "GB/s", bound: str = "hbm") -> list:
+        """[value, ms per step, roofline achieved, roofline frac, launches]"""
+        r = R[key]
+        ro = roof(r, key, bound)
+        return [rnd(r["value"]), rnd(r["ms_per_step"]), ro["achieved"], ro["frac"], r.get("launches_per_step", 1)]
+
     q40 = R["gemv_q4_0_11008x4096_b1"]
-    sweep = R["gemm_sweep"]
+    probe = R["read_q4_0_11008x4096"]
     gg = R["gguf_upload"]
     line = {
         "metric": METRIC,
-        "value": q40["value"],
+        "value": rnd(q40["value"]),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": q40["steps"],
         "warmup": args.warmup,
-        "ms_per_step": q40["ms_per_step"],
+        "ms_per_step": rnd(q40["ms_per_step"]),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -667,61 +655,34 @@ def main() -> int:
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
                    "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches",
                    "x_repr": X_REPR},
-        "roofline": roof_hbm("gemv_q4_0_11008x4096_b1"),
+        "roofline": roof(q40, "gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
-        "secondary": [
-            gemv_line("gemv_q4_0_11008x4096_b1_f32x", "Q4_0 GEMV 11008x4096 batch 1, x kept in f32 (VX_GEMV_X_F32: "
-                      "f32 FMA on the exactly decoded weights)", "f32"),
-        ] + [gemv_line(k, v[4], DT_INT8X) for k, v in GEMV_SECONDARY.items()] + [
-            gemv_line("gemv_f32_11008x4096", "f32 GEMV y = A x, A 11008x4096 row-major (the GEMM op's N == 1 route, "
-                      "vx_gemv_f32), A rotating over >= 512 MB, HIP-graph replay", "f32"),
-            gemv_line("gemv_f32_1552x4096", "read-only HBM stream of the headline's size: vx_gemv_f32 on A 1552x4096 "
-                      "f32 (25.43 MB read per launch; the Q4_0 GEMV reads 25.42 MB), A rotating over >= 512 MB, "
-                      "HIP-graph replay (the achievable read rate of one launch this size)", "f32"),
-            gemv_line("gemv_f32_32768x4096", "read-only HBM stream, 537 MB per launch: vx_gemv_f32 on A 32768x4096 "
-                      "f32 (the achievable read rate of a long stream)", "f32"),
-            {"workload": "contiguous copy of a transposed 8192x8192 f32 view (Contiguous::launch)",
-             "value": R["contiguous_t8192"]["value"], "unit": "GB/s",
-             "ms_per_step": R["contiguous_t8192"]["ms_per_step"], "roofline": roof_hbm("contiguous_t8192")},
-            {"workload": "streaming copy: Contiguous::launch of a contiguous 8192x8192 f32 view (achievable HBM "
-                         "bandwidth of a plain read + write stream on this GPU)",
-             "value": R["copy_8192"]["value"], "unit": "GB/s", "ms_per_step": R["copy_8192"]["ms_per_step"],
-             "roofline": roof_hbm("copy_8192")},
-            {"workload": "streaming copy of the headline's size: Contiguous::launch of a contiguous 3104x1024 f32 "
-                         "view, 25.43 MB read + written per launch (the headline GEMV moves 25.42 MB), sources "
-                         "rotating over >= 512 MB, HIP-graph replay (the achievable rate of one launch this size)",
-             "value": R["copy_3104x1024"]["value"], "unit": "GB/s", "ms_per_step": R["copy_3104x1024"]["ms_per_step"],
-             "roofline": roof_hbm("copy_3104x1024")},
-        ] + [
-            {"workload": f"quantize f32 14336x4096 to {label} blocks (ggml reference quantizer)",
-             "value": R[k]["value"], "unit": "GB/s", "ms_per_step": R[k]["ms_per_step"], "roofline": roof_hbm(k),
-             **({"note": "VALU-bound: ggml's 21-candidate scale/min search per 32-value sub-block, one "
-                         "sub-block per lane, 11-13k VALU instructions per wave (ISA count): 0.53-0.59 ms at one "
-                         "wave-instruction per CU per cycle (256 CUs, 2.4 GHz); the HBM fraction is not its bound"}
-                if label == "Q4_K" else {})}
-            for k, label in (("quantize_q8_0_14336x4096", "Q8_0"), ("quantize_q4_k_14336x4096", "Q4_K"))
-        ] + [
-            {"workload": "GGUF file (page cache) -> HBM upload, 1.14 GB data section (vx_gguf_upload)",
-             "value": gg["value"], "unit": "GB/s", "ms_per_step": gg["ms_per_step"], "open_ms": gg["open_ms"],
-             "roofline": {"bound": "pcie", "achieved": gg["value"], "peak": PCIE_PEAK_GBS, "unit": "GB/s",
-                          "frac": gg["value"] / PCIE_PEAK_GBS, "traffic": None}},
-        ] + [
-            {"workload": v[4], "value": R[k]["value"], "unit": "TFLOP/s", "ms_per_step": R[k]["ms_per_step"],
-             "roofline": roof_mfma(k),
-             **({"cpu_baseline": cpu["gemm4096"], "cpu_baseline_1024": cpu["gemm1024"]} if cpu and k == "gemm_f32_4096"
-                else {"cpu_baseline": cpu["gemm4096x11008"]} if cpu and k == "gemm_f32_4096x11008x4096" else {})}
-            for k, v in GEMMS.items()
-        ] + [
-            {"workload": "broadcast f32 GEMM out[b] = A[b] W + out[b], A [8, 1024, 4096], shared W [4096, 4096] "
-                         "(vx_gemm_f32_ex, beta = 1)", "value": R["gemm_f32_broadcast_8x1024"]["value"],
-             "unit": "TFLOP/s", "ms_per_step": R["gemm_f32_broadcast_8x1024"]["ms_per_step"],
-             "roofline": roof_mfma("gemm_f32_broadcast_8x1024")},
-            {"workload": "f32 GEMM sweep of the reference's benchmark (examples/gemm_bench.rs: dim^3 for dim in "
-                         "64..4096, 3 warmup + 10 timed launches each), default tiled route and naive kernel",
-             "unit": "TFLOP/s", "value": sweep[-1]["tiled_tflops"], "points": sweep},
-        ],
+        "q8_0_b1": gline("gemv_q8_0_4096x4096_b1", "Q8_0 GEMV 4096x4096 b=1 (the metric's other format)"),
+        "q4_0_b1_f32x": gline("gemv_q4_0_11008x4096_b1_f32x", "headline config, x kept in f32 (VX_GEMV_X_F32)"),
+        "read_ceiling": dict(gline("read_q4_0_11008x4096", "vx_gemv_q_read_probe: the headline GEMV's loads of W "
+                                   "alone (no x, no arithmetic), 25.4 MB"),
+                             gemv_over_probe=rnd(q40["step_ms_events"] / probe["step_ms_events"], 3)),
+        "read_ceiling_q8_0": gline("read_q8_0_4096x4096", "vx_gemv_q_read_probe on Q8_0 4096x4096"),
+        "gemm_4096": dict(gline("gemm_f32_4096", GEMMS["gemm_f32_4096"][4], "TFLOP/s", "mfma"),
+                          steps=GEMM_STEPS, warmup=GEMM_WARMUP,
+                          cpu_baseline=cpu["gemm4096"] if cpu else None),
+        # compact lines: key -> [value, ms per step, roofline achieved, roofline frac, launches per step]
+        "lines_fields": ["value", "ms_per_step", "roof_achieved", "roof_frac", "launches"],
+        "lines_gbs": {k: short(k) for k in GEMV_SECONDARY},
+        "lines_gbs_other": {k: short(k) for k in ("split_x_11008_b8", "split_x_4096_b16", "gemv_f32_11008x4096",
+                                                   "gemv_f32_1552x4096", "gemv_f32_32768x4096", "contiguous_t8192",
+                                                   "copy_8192", "copy_3104x1024", "quantize_q8_0_14336x4096",
+                                                   "quantize_q4_k_14336x4096")},
+        "lines_tflops": {k: short(k, "TFLOP/s", "mfma") for k in ("gemm_f32_4096x11008x4096", "gemm_f32_4096_transb",
+                                                                   "gemm_f32_broadcast_8x1024")},
+        "gguf_upload": {"value": rnd(gg["value"]), "unit": "GB/s", "ms": rnd(gg["ms_per_step"]),
+                        "pcie_frac": rnd(gg["value"] / PCIE_PEAK_GBS, 3)},
+        "gemm_sweep": {"fields": ["dim", "tiled_tflops", "naive_tflops"],
+                       "points": [[d, rnd(t, 3), rnd(n, 3)] for d, t, n in R["gemm_sweep"]]},
+        "cpu_baselines": {k: {"value": rnd(v["value"]), "unit": v["unit"], "cores": v["cores"]}
+                          for k, v in (cpu or {}).items() if k != "q4_0"},
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     return 0
 
 

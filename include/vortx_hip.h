@@ -15,10 +15,13 @@
  *  - Launches are asynchronous on the given stream (NULL = null stream).
  *    The caller keeps every buffer alive until the stream work completes;
  *    the library never frees or retains caller memory.
- *  - A vx_ctx may be shared by threads. Its one piece of mutable state is
- *    the activation workspace of vx_gemv_q / vx_gemv_q_ex at B >= 2 (see
- *    there): such calls on one context must not overlap in time on
- *    different streams.
+ *  - A vx_ctx is immutable after vx_init and may be shared by threads and
+ *    streams (as the reference's `Gemm` is `&self`). No entry point of this
+ *    header allocates, frees or synchronizes device memory after vx_init,
+ *    except vx_gemv_q_noalloc's shared scratch array (see there): memory a
+ *    call needs beyond its operands is passed in by the caller
+ *    (vx_gemv_q_ws), like the reference's caller-owned
+ *    `shapes: &mut TensorLayoutBuffers` (src/linalg/gemm.rs:47-56).
  */
 #ifndef VORTX_HIP_H
 #define VORTX_HIP_H
@@ -207,16 +210,15 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
  * one f32 scale (|error| <= ~1.6e-5 of the block's max|x|), the products
  * with the weights are exact int32 and the scaling and accumulation are
  * f32. vx_gemv_q_ex(..., VX_GEMV_X_F32) keeps x in f32.
- * With 2 <= B <= 8, K <= 4096 and x of stride 1 along K with 16-byte
- * aligned columns, the batched kernels split x themselves (one launch, no
- * workspace). Otherwise, with B >= 2 (fast layouts), x is split by
- * vx_quantize_x into a workspace the context owns (allocated on first use
- * and grown when a call needs more; growing synchronizes the device), then
- * vx_gemv_q_xq runs: calls of one context must therefore not overlap in time
- * on different streams, and the first call of a given size must not be made
- * during stream capture (VX_ERR_UNSUPPORTED then). Both give the same bits.
- * Callers that cannot allocate use vx_gemv_q_noalloc or vx_quantize_x +
- * vx_gemv_q_xq on buffers of their own. */
+ * Batches (B >= 2) run on the int8 matrix cores; where the GEMV kernel
+ * can split x itself (2 <= B <= 8, K <= 4096 — one 256-element item per
+ * wave — and x of stride 1 along K with 16-byte aligned columns) that is one
+ * launch. Other batched shapes need the split in device memory: this entry
+ * point has none, so they are computed with x kept in f32 (the
+ * VX_GEMV_X_F32 kernels); vx_gemv_q_ws with a caller workspace keeps the
+ * int8 split there (the fused and the two-launch route give the same bits).
+ * Uses no memory beyond its operands; safe to call concurrently on any
+ * streams, and to capture. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
               const vx_qweight* w, const vx_cview* x);
 
@@ -229,8 +231,36 @@ int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
  * keeps x in f32 instead (f32 FMA on the exactly decoded weights; slower);
  * VX_GEMV_X_INT8 names the default split and may not be combined with it. */
 typedef enum vx_gemv_flags { VX_GEMV_X_INT8 = 1, VX_GEMV_X_F32 = 2 } vx_gemv_flags;
+/* With VX_GEMV_X_INT8, a batched shape whose split needs device memory
+ * (see vx_gemv_q) returns VX_ERR_UNSUPPORTED here instead of falling back
+ * to f32 x. */
 int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_cview* x, uint32_t flags);
+
+/* vx_gemv_q_ex with a device workspace owned by the caller. No counterpart
+ * in the reference (it has no quantized code); the workspace plays the part
+ * of Gemm::dispatch's caller-owned `shapes: &mut TensorLayoutBuffers`
+ * (src/linalg/gemm.rs:47-56): per-caller mutable state kept outside the
+ * (immutable) context. Where a batched call needs its activation split in
+ * memory (see vx_gemv_q), x is split into `workspace` by the vx_quantize_x
+ * kernel and the GEMV reads it (two launches on `stream`); elsewhere the
+ * workspace is not touched. workspace: device memory, 16-byte aligned, at
+ * least vx_gemv_q_ws_size(...) bytes (a smaller non-NULL workspace is
+ * VX_ERR_INVALID; NULL behaves as vx_gemv_q_ex). The library never
+ * allocates, frees or retains it; its contents need not start at zero.
+ * Calls that share one workspace must be ordered (one stream, or events);
+ * calls with different workspaces may run concurrently on any streams of
+ * one context. A captured HIP graph records the workspace address: keep the
+ * buffer alive and unshared while the graph can be replayed. */
+int vx_gemv_q_ws(vx_ctx ctx, vx_stream stream, const vx_mview* y,
+                 const vx_qweight* w, const vx_cview* x, uint32_t flags,
+                 void* workspace, uint64_t workspace_bytes);
+
+/* Workspace bytes vx_gemv_q_ws may use for W of `qtype` with K columns
+ * and B batch columns under `flags`: vx_xq_size(K, B) for the int8 route at
+ * B >= 2 (K a multiple of 64), else 0 (it needs none). */
+int vx_gemv_q_ws_size(uint32_t qtype, uint32_t K, uint32_t B, uint32_t flags,
+                      uint64_t* bytes);
 
 /* ---- activation split: x -> two int8 levels per 32-block (VX_XQ) -----
  * No counterpart in the reference (it has no quantized code): the step
@@ -280,11 +310,13 @@ int vx_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* out, const vx_cview
 int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                  const vx_qweight* w, const vx_xq* x);
 
-/* vx_gemv_q_ex that allocates nothing. No counterpart in the reference:
- * for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * arguments, flags, kernels and results as vx_gemv_q_ex; where that one
- * splits x into the context's workspace (B >= 2), this one uses a fixed
+/* vx_gemv_q_ws without a caller workspace, allocating nothing. No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc) yet want the int8 split at every batched shape. Same
+ * arguments and flags as vx_gemv_q_ex, and the kernels and results of
+ * vx_gemv_q_ws: where that one splits x into the caller's workspace
+ * (B >= 2), this one uses a fixed
  * device array of VX_NOALLOC_SCRATCH_BYTES (4 MiB) that the library's GEMV
  * code object holds per context from vx_init to vx_destroy, so the split of
  * x, vx_xq_size(K, B) bytes (72 per 32 elements of x), must fit it (else
@@ -296,6 +328,16 @@ int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y,
 #define VX_NOALLOC_SCRATCH_BYTES (4u << 20)
 int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y,
                       const vx_qweight* w, const vx_cview* x, uint32_t flags);
+
+/* Measurement only, no counterpart in the reference: the loads of the
+ * batch-1 GEMV (vx_gemv_q at B = 1) with nothing else — the same grid, row
+ * order and per-lane 64-weight units, every item of a round of four in
+ * flight, no x, no barrier, no arithmetic. Reads every byte of W once and
+ * writes one word per row to y[0..M) (contents unspecified). Its time is
+ * the ceiling of what that access pattern streams in one launch. Needs K a
+ * multiple of 64 and 4-byte aligned rows (else VX_ERR_UNSUPPORTED). */
+int vx_gemv_q_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w,
+                         float* y);
 
 /* out[m, k] = W[m, k] decoded to f32 (bit-exact: every block value is
  * exactly representable in f32). out is an [M, K] view, any strides. */

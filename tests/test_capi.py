@@ -104,3 +104,17 @@ def test_init_without_gpu_fails_cleanly():
     s = vx.lib().vx_init(0, C.byref(h))
     assert s in (_ffi.VX_ERR_HIP, _ffi.VX_ERR_INVALID) and not h.value
     assert vx.lib().vx_last_error_message()
+
+
+def test_gemv_q_ws_size():
+    """Workspace bytes of vx_gemv_q_ws: the activation split (vx_xq_size) on
+    the int8 route at B >= 2, nothing at B = 1, with f32 x or K % 64 != 0."""
+    L = vx.lib()
+    n = C.c_uint64()
+    for qt, K, B, flags, want in [(vx.VX_Q4_0, 4096, 8, 0, vx.xq_size(4096, 8)),
+                                  (vx.VX_Q4_K, 4096, 16, 0, vx.xq_size(4096, 16)),
+                                  (vx.VX_Q8_0, 11008, 3, 1, vx.xq_size(11008, 3)),
+                                  (vx.VX_Q4_0, 4096, 1, 0, 0), (vx.VX_Q4_0, 4096, 8, 2, 0), (vx.VX_Q4_0, 96, 4, 0, 0)]:
+        assert L.vx_gemv_q_ws_size(qt, K, B, flags, C.byref(n)) == 0
+        assert n.value == want, (qt, K, B, flags)
+    assert L.vx_gemv_q_ws_size(3, 4096, 8, 0, C.byref(n)) == _ffi.VX_ERR_INVALID

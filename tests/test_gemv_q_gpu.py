@@ -65,13 +65,17 @@ def test_dequantize_strided_output(qgemv, qtype):
     assert torch.isnan(big[:, 0::2]).all(), "wrote outside the view"
 
 
-def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False, x_f32=False):
+def _run_gemv(qgemv, qtype, M, K, B, seed=0, x_kb=None, y_out=None, x_int8=False, x_f32=False, ws=True):
+    """One GEMV; ws: with a workspace (vx_gemv_q_ws, the int8 split at every
+    batched shape) or without (vx_gemv_q_ex)."""
     w = S.quant_weights(qtype, M, K, seed=seed, device=DEV)
     x = S.activations(B, K, seed=seed + 1, device=DEV)
     y = torch.full((B, M), float("nan"), device=DEV) if y_out is None else y_out
     xv = x.t() if x_kb is None else x_kb(x)
     yv = y.t() if y_out is None else y
-    qgemv.dispatch(yv, vx.QWeight(w, qtype, M, K), xv, x_int8=x_int8, x_f32=x_f32)
+    qw = vx.QWeight(w, qtype, M, K)
+    wsp = vx.QuantGemv.workspace(qw, B) if ws else None
+    qgemv.dispatch(yv, qw, xv, x_int8=x_int8, x_f32=x_f32, workspace=wsp)
     torch.cuda.synchronize()
     ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
     return yv.cpu().numpy(), ref
@@ -177,14 +181,16 @@ def test_gemv_batched_x_edge_values(qgemv, qtype, B):
     x[0::2, 64:96] *= 1e30
     x[:, 96:128] *= 1e-3
     x[:, 100] = 50.0
-    y = torch.full((B, M), float("nan"), device=DEV)
-    qgemv.dispatch(y.t(), vx.QWeight(w, qtype, M, K), x.t())
-    torch.cuda.synchronize()
     ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
-    got = y.cpu().numpy().T
-    for b in range(B):
-        assert_close(got[:, b], ref[:, b], what=f"column {b}")
-        assert_close(got[:, b], ref[:, b], tol=2e-4, what=f"column {b} (two-level bound)")
+    qw = vx.QWeight(w, qtype, M, K)
+    for wsp in (None, vx.QuantGemv.workspace(qw, B)):
+        y = torch.full((B, M), float("nan"), device=DEV)
+        qgemv.dispatch(y.t(), qw, x.t(), workspace=wsp)
+        torch.cuda.synchronize()
+        got = y.cpu().numpy().T
+        for b in range(B):
+            assert_close(got[:, b], ref[:, b], what=f"column {b}")
+            assert_close(got[:, b], ref[:, b], tol=2e-4, what=f"column {b} (two-level bound)")
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
@@ -289,12 +295,13 @@ def test_non_finite_x_reaches_its_column_only(qgemv, qtype, B, bad):
     note(f"gemv non-finite x {QN[qtype]} B={B} {bad}")
     w = vx.QWeight(S.quant_weights(qtype, M, K, seed=5, device=DEV), qtype, M, K)
     x = S.activations(B, K, seed=6, device=DEV)
+    wsp = vx.QuantGemv.workspace(w, B)
     y0 = torch.empty((B, M), device=DEV)
-    qgemv.dispatch(y0.t(), w, x.t())
+    qgemv.dispatch(y0.t(), w, x.t(), workspace=wsp)
     xb = x.clone()
     xb[0, 777] = bad
     y = torch.empty((B, M), device=DEV)
-    qgemv.dispatch(y.t(), w, xb.t())
+    qgemv.dispatch(y.t(), w, xb.t(), workspace=wsp)
     torch.cuda.synchronize()
     assert not torch.isfinite(y[0]).any(), "a non-finite x value was lost"
     if B > 1:
@@ -322,3 +329,98 @@ def test_non_finite_x_other_paths(qgemv, qtype, path, bad):
     assert not torch.isfinite(y[0]).any(), "a non-finite x value was lost"
     if B > 1:
         assert torch.isfinite(y[1:]).all()
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_gemv_without_workspace(qgemv, qtype):
+    """vx_gemv_q_ex without a workspace: batched shapes the GEMV kernel can
+    split itself (one item per wave, <= 8 columns, x of stride 1 along K)
+    give the bits of the workspace route; the others keep x in f32 (held to
+    the f32 kernels' 1e-5), or, asked for the int8 split explicitly, fail
+    with VX_ERR_UNSUPPORTED and launch nothing."""
+    M = 300
+    # (K, B, fused): one item per wave and <= 8 columns fuse; 16 columns
+    # (two column groups) or K past 4096 (several items) need the split
+    for K, B, fused in ((4096, 4, True), (2048, 8, True), (4096, 16, False), (8192, 3, False)):
+        note(f"gemv no-workspace {QN[qtype]} K={K} B={B}")
+        w = torch.from_numpy(S.quant_weights(qtype, M, K, seed=42 + K).numpy()).to(DEV)
+        qw = vx.QWeight(w, qtype, M, K)
+        x = S.activations(B, K, seed=43, device=DEV)
+        y0 = torch.full((B, M), float("nan"), device=DEV)
+        y1 = torch.full((B, M), float("nan"), device=DEV)
+        qgemv.dispatch(y0.t(), qw, x.t(), workspace=vx.QuantGemv.workspace(qw, B))
+        qgemv.dispatch(y1.t(), qw, x.t())
+        torch.cuda.synchronize()
+        ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())
+        assert_close(y0.cpu().numpy().T, ref, what="workspace route")
+        if fused:
+            assert torch.equal(y0.view(torch.int32), y1.view(torch.int32)), "fused route differs from the split"
+        else:
+            assert_close(y1.cpu().numpy().T, ref, tol=1e-5, what="f32-x fallback")
+            y2 = torch.full((B, M), float("nan"), device=DEV)
+            with pytest.raises(vx.VortxError, match="VX_ERR_UNSUPPORTED"):
+                qgemv.dispatch(y2.t(), qw, x.t(), x_int8=True)
+            torch.cuda.synchronize()
+            assert torch.isnan(y2).all(), "a refused call wrote y"
+
+
+def test_gemv_workspace_errors(qgemv):
+    M, K, B = 64, 8192, 4
+    qw = vx.QWeight(S.quant_weights(vx.VX_Q4_0, M, K, seed=1, device=DEV), vx.VX_Q4_0, M, K)
+    x = S.activations(B, K, seed=2, device=DEV)
+    y = torch.empty((B, M), device=DEV)
+    need = vx.QuantGemv.workspace_size(qw, B)
+    assert need == vx.xq_size(K, B) and vx.QuantGemv.workspace_size(qw, 1) == 0
+    assert vx.QuantGemv.workspace_size(qw, B, x_f32=True) == 0
+    small = torch.empty(need - 16, dtype=torch.uint8, device=DEV)
+    with pytest.raises(vx.VortxError, match="VX_ERR_INVALID"):
+        qgemv.dispatch(y.t(), qw, x.t(), workspace=small)
+    big = torch.empty(need + 16, dtype=torch.uint8, device=DEV)
+    with pytest.raises(vx.VortxError, match="VX_ERR_INVALID"):  # not 16-byte aligned
+        qgemv.dispatch(y.t(), qw, x.t(), workspace=big[4:])
+
+
+def test_gemv_two_streams_own_workspaces(qgemv):
+    """One context, two streams, each with its own workspace, running
+    interleaved batched GEMVs that need the split in memory: every result
+    equals the serial run bit for bit (the context holds no per-call state)."""
+    cases = [(vx.VX_Q4_K, 2048, 4096, 16), (vx.VX_Q4_0, 1024, 11008, 8), (vx.VX_Q8_0, 512, 8192, 12)]
+    data = []
+    for i, (qt, M, K, B) in enumerate(cases):
+        qw = vx.QWeight(S.quant_weights(qt, M, K, seed=50 + i, device=DEV), qt, M, K)
+        data.append((qw, S.activations(B, K, seed=60 + i, device=DEV), B, M))
+    serial = []
+    ws0 = torch.empty(max(vx.QuantGemv.workspace_size(qw, B) for qw, _, B, _ in data), dtype=torch.uint8, device=DEV)
+    for qw, x, B, M in data:
+        y = torch.empty((B, M), device=DEV)
+        qgemv.dispatch(y.t(), qw, x.t(), workspace=ws0)
+        serial.append(y)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [torch.empty_like(ws0), torch.empty_like(ws0)]
+    outs = [[torch.full((B, M), float("nan"), device=DEV) for qw, x, B, M in data] for _ in range(2)]
+    torch.cuda.current_stream().synchronize()
+    for rep in range(4):
+        for si in (0, 1):
+            for ci in (range(len(data)) if si == 0 else reversed(range(len(data)))):
+                qw, x, B, M = data[ci]
+                qgemv.dispatch(outs[si][ci].t(), qw, x.t(), stream=streams[si], workspace=wss[si])
+    torch.cuda.synchronize()
+    for si in (0, 1):
+        for ci in range(len(data)):
+            assert torch.equal(outs[si][ci].view(torch.int32), serial[ci].view(torch.int32)), (si, ci)
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("M,K", [(11008, 4096), (37, 8192), (4096, 4096)])
+def test_read_probe_stays_in_its_rows(qgemv, qtype, M, K):
+    """vx_gemv_q_read_probe (measurement kernel) writes exactly y[0..M)."""
+    if K % O.QTYPE_INFO[qtype][0]:
+        pytest.skip("K not a multiple of the block size")
+    note(f"read probe {QN[qtype]} {M}x{K}")
+    qw = vx.QWeight(S.quant_weights(qtype, M, K, seed=3, device=DEV), qtype, M, K)
+    y = torch.full((M + 64,), float("nan"), device=DEV)
+    qgemv.read_probe(y, qw)
+    torch.cuda.synchronize()
+    assert not torch.isnan(y[:M]).any(), "a row was not written"
+    assert torch.isnan(y[M:]).all(), "wrote past the rows"

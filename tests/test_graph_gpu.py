@@ -12,17 +12,20 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-@pytest.mark.parametrize("B", [1, 4, 16])
-def test_gemv_graph_replay_matches_eager(qgemv, B):
-    M, K, n = 300, 1024, 6
-    note(f"graph replay gemv B={B}")
+@pytest.mark.parametrize("B,use_ws", [(1, False), (4, False), (16, False), (16, True), (5, True)])
+def test_gemv_graph_replay_matches_eager(qgemv, B, use_ws):
+    """use_ws: one caller workspace shared by the captured launches (one
+    stream, so in order); at B = 16 and at K = 8192 the split goes there."""
+    M, K, n = 300, 8192 if B == 5 else 1024, 6
+    note(f"graph replay gemv B={B} workspace={use_ws}")
     ws = [S.quant_weights(vx.VX_Q4_K if B == 16 else vx.VX_Q4_0, M, K, seed=i, device=DEV) for i in range(n)]
     qt = vx.VX_Q4_K if B == 16 else vx.VX_Q4_0
     xs = [S.activations(B, K, seed=50 + i, device=DEV) for i in range(n)]
     ys = [torch.full((B, M), float("nan"), device=DEV) for _ in range(n)]
+    wsp = vx.QuantGemv.workspace(vx.QWeight(ws[0], qt, M, K), B) if use_ws else None
     eager = []
     for i in range(n):
-        qgemv.dispatch(ys[i].t(), vx.QWeight(ws[i], qt, M, K), xs[i].t())
+        qgemv.dispatch(ys[i].t(), vx.QWeight(ws[i], qt, M, K), xs[i].t(), workspace=wsp)
     torch.cuda.synchronize()
     eager = [y.clone() for y in ys]
     s = torch.cuda.Stream()
@@ -30,7 +33,7 @@ def test_gemv_graph_replay_matches_eager(qgemv, B):
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
             for i in range(n):
-                qgemv.dispatch(ys[i].t(), vx.QWeight(ws[i], qt, M, K), xs[i].t(), stream=s)
+                qgemv.dispatch(ys[i].t(), vx.QWeight(ws[i], qt, M, K), xs[i].t(), stream=s, workspace=wsp)
     for rep in range(3):
         for y in ys:
             y.fill_(float("nan"))

@@ -162,7 +162,7 @@ def test_one_split_for_three_matrices(qgemv):
         y1 = torch.empty((B, M), device=DEV)
         y2 = torch.empty((B, M), device=DEV)
         qgemv.dispatch_xq(y1.t(), w, q)
-        qgemv.dispatch(y2.t(), w, x.t())
+        qgemv.dispatch(y2.t(), w, x.t(), workspace=vx.QuantGemv.workspace(w, B))
         torch.cuda.synchronize()
         assert torch.equal(y1.view(torch.int32), y2.view(torch.int32)), QN[qtype]
 
@@ -195,8 +195,8 @@ def test_xq_errors(qgemv):
                                    (300, 4096, 4), (257, 832, 3), (40, 2048, 4)])
 def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
     """vx_gemv_q with x stored [B, K] (stride 1 along K) splits x inside the
-    GEMV kernels (one launch); stored [K, B] it runs vx_quantize_x, then the
-    GEMV on the split. Same bytes of x, same kernels otherwise: y is equal bit
+    GEMV kernels (one launch); stored [K, B] it runs vx_quantize_x into the
+    caller's workspace, then the GEMV on the split. Same bytes of x, same kernels otherwise: y is equal bit
     for bit. (The host fuses only one item and one group of 8 columns per
     wave, B <= 8 with K <= 4096; the other shapes check that both storages
     take the split path and agree.)"""
@@ -211,8 +211,9 @@ def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
     xkb = x.t().contiguous()  # [K, B] storage: stride B along K
     y1 = torch.full((B, M), float("nan"), device=DEV)
     y2 = torch.full((B, M), float("nan"), device=DEV)
-    qgemv.dispatch(y1.t(), w, x.t())
-    qgemv.dispatch(y2.t(), w, xkb)
+    wsp = vx.QuantGemv.workspace(w, B)  # [K, B] storage: the split goes to the workspace
+    qgemv.dispatch(y1.t(), w, x.t(), workspace=wsp)
+    qgemv.dispatch(y2.t(), w, xkb, workspace=wsp)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
     ref = O.gemv_q_f64(qtype, w.data.cpu().numpy(), M, K, x.cpu().numpy())
@@ -232,8 +233,9 @@ def test_fused_split_non_finite_column(qgemv, B, bad):
     x[bad[1], 3000] = float("inf")
     y1 = torch.empty((B, M), device=DEV)
     y2 = torch.empty((B, M), device=DEV)
-    qgemv.dispatch(y1.t(), w, x.t())
-    qgemv.dispatch(y2.t(), w, x.t().contiguous())
+    wsp = vx.QuantGemv.workspace(w, B)  # [K, B] storage: the split goes to the workspace
+    qgemv.dispatch(y1.t(), w, x.t(), workspace=wsp)
+    qgemv.dispatch(y2.t(), w, x.t().contiguous(), workspace=wsp)
     torch.cuda.synchronize()
     good = [c for c in range(B) if c not in bad]
     fin = torch.isfinite(y1)
@@ -271,8 +273,9 @@ def test_batched_random_shapes(qgemv, qtype, M, K, B):
     x = S.activations(B, K, seed=M + 3 * B, device=DEV)
     y1 = torch.full((B, M), float("nan"), device=DEV)
     y2 = torch.full((B, M), float("nan"), device=DEV)
-    qgemv.dispatch(y1.t(), w, x.t())
-    qgemv.dispatch(y2.t(), w, x.t().contiguous())
+    wsp = vx.QuantGemv.workspace(w, B)  # [K, B] storage: the split goes to the workspace
+    qgemv.dispatch(y1.t(), w, x.t(), workspace=wsp)
+    qgemv.dispatch(y2.t(), w, x.t().contiguous(), workspace=wsp)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
     ref = O.gemv_q_f64(qtype, w.data.cpu().numpy(), M, K, x.cpu().numpy())

@@ -326,15 +326,52 @@ class QuantGemv(_Context):
         yv, wc, q = _view_of(y, True), w._c(), xq._c()
         check(lib().vx_gemv_q_xq(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(q)))
 
-    def dispatch(self, y, w: QWeight, x, stream=None, x_f32: bool = False, x_int8: bool = False) -> None:
+    @staticmethod
+    def workspace_size(w: "QWeight", B: int, x_f32: bool = False) -> int:
+        """Bytes of workspace ``dispatch(..., workspace=)`` may use for B
+        columns (vx_gemv_q_ws_size; 0: none)."""
+        n = C.c_uint64()
+        check(lib().vx_gemv_q_ws_size(w.qtype, w.cols, B, _ffi.VX_GEMV_X_F32 if x_f32 else 0, C.byref(n)))
+        return n.value
+
+    @staticmethod
+    def workspace(w: "QWeight", B: int, device="cuda:0"):
+        """A device workspace for ``dispatch`` on W with B columns (a uint8
+        tensor; torch's allocator owns it, the library never does)."""
+        import torch
+        return torch.empty(max(16, QuantGemv.workspace_size(w, B)), dtype=torch.uint8, device=device)
+
+    def dispatch(self, y, w: QWeight, x, stream=None, x_f32: bool = False, x_int8: bool = False,
+                 workspace=None) -> None:
         """y = W x. By default x is split per 32-block into two int8 levels
         (error <= 1.6e-5 of the block's max|x|) and every product is exact in
         int32 (include/vortx_hip.h, vx_gemv_q_ex). ``x_f32=True`` keeps x in
         f32 (f32 FMA on the exactly decoded weights); ``x_int8=True`` names
-        the default explicitly."""
+        the default explicitly. ``workspace``: a uint8 GPU tensor of at least
+        ``workspace_size(w, B)`` bytes (vx_gemv_q_ws), where batched shapes
+        split x when the GEMV kernel cannot split it itself; without one
+        those shapes keep x in f32 (or, with ``x_int8``, raise)."""
         yv, xv, wc = _view_of(y, True), _view_of(x, False), w._c()
         flags = (_ffi.VX_GEMV_X_F32 if x_f32 else 0) | (_ffi.VX_GEMV_X_INT8 if x_int8 else 0)
-        check(lib().vx_gemv_q_ex(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags))
+        if workspace is None:
+            check(lib().vx_gemv_q_ex(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags))
+            return
+        import torch
+        if not (isinstance(workspace, torch.Tensor) and workspace.is_cuda and workspace.is_contiguous()):
+            raise TypeError("workspace must be a contiguous GPU tensor")
+        nbytes = workspace.numel() * workspace.element_size()
+        check(lib().vx_gemv_q_ws(self._h, _stream(stream), C.byref(yv), C.byref(wc), C.byref(xv), flags,
+                                 workspace.data_ptr(), nbytes))
+
+    def read_probe(self, y, w: QWeight, stream=None) -> None:
+        """The batch-1 GEMV's loads of W alone (vx_gemv_q_read_probe), one
+        word per row to the f32 GPU tensor y (measurement only)."""
+        import torch
+        if not (isinstance(y, torch.Tensor) and y.is_cuda and y.dtype == torch.float32 and y.is_contiguous()
+                and y.numel() >= w.rows):
+            raise TypeError("y must be a contiguous float32 GPU tensor of at least w.rows elements")
+        wc = w._c()
+        check(lib().vx_gemv_q_read_probe(self._h, _stream(stream), C.byref(wc), y.data_ptr()))
 
     def quantize(self, out: "QWeight", x, stream=None) -> None:
         """Write the blocks of ``out`` from the f32 [rows, cols] view ``x``

@@ -702,6 +702,55 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         if (nfull + (uint32_t)j < nitems) body(nfull + (uint32_t)j, wr[j]);
 }
 
+// Read probe (measurement only): the loads of vx_gemv_p1i with nothing
+// else. Same grid, wave-major row numbering and per-lane units; no x, no
+// barrier, no arithmetic; every item of a round of P in flight before any is
+// used (an empty asm statement consumes each loaded word, so the loads stay
+// and their waits are real). Lane 0 writes its XOR of the row's words to y:
+// the bytes of the GEMV without x. Its time is the ceiling of what the
+// GEMV's access pattern can stream in one launch.
+template <int QT, int P>
+__device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a) {
+    constexpr int NW = vx_unit<QT>::NW;
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t nwv = gridDim.x * 16u;
+    const uint32_t gw = wave * gridDim.x + blockIdx.x;
+    const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
+    const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
+    const uint32_t nitems = nrows * npass;
+    uint32_t acc = 0u;
+    for (uint32_t it0 = 0; it0 < nitems; it0 += P) {
+        uint32_t wr[P][NW];
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            // past the wave's last item every lane reads the matrix's first
+            // unit (one cache line), as the GEMV's ring does
+            const bool past = it0 + (uint32_t)j >= nitems;  // wave-uniform
+            const uint32_t it = min(it0 + (uint32_t)j, nitems - 1u);
+            const uint32_t ri = it / npass, p = it - ri * npass;
+            vx_load_unit<QT, true>(past ? a.w : a.w + (uint64_t)(gw + ri * nwv) * a.row_stride,
+                                   past ? 0u : min(64u * p + lane, nunits - 1u), wr[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const uint32_t it = it0 + (uint32_t)j;
+#pragma unroll
+            for (int q = 0; q < NW; ++q) {
+                asm volatile("" ::"v"(wr[j][q]));
+                acc ^= wr[j][q];
+            }
+            if (it < nitems) {
+                const uint32_t ri = it / npass, p = it - ri * npass;
+                if (p == npass - 1u) {
+                    if (lane == 0) a.y[(int64_t)(gw + ri * nwv) * a.ys_m] = __uint_as_float(acc & 0x007FFFFFu);
+                    acc = 0u;
+                }
+            }
+        }
+    }
+}
+
 // Batch NB > 1: lane l serves row group g = l / LPR (R rows each) and unit
 // l % LPR of each pass; weights are decoded exactly 8 at a time and
 // multiplied with the matching x slots of every batch column from LDS.
@@ -882,6 +931,13 @@ VX_GEMV_P1I(VX_Q4_0, q4_0, 2)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
+#define VX_READ_PROBE(QT, QN)                                                                     \
+    extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(vx_gemv_args a) {      \
+        vx_read_probe<QT, 4>(a);                                                                  \
+    }
+VX_READ_PROBE(VX_Q4_0, q4_0)
+VX_READ_PROBE(VX_Q8_0, q8_0)
+VX_READ_PROBE(VX_Q4_K, q4_k)
 
 // ------------------------------------------------------------------------
 // Batched GEMV on split activations (vx_xq, written once per call by

@@ -14,7 +14,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <mutex>
 #include <algorithm>
 #include <cmath>
 #include <string>
@@ -85,10 +84,8 @@ struct vx_context {
     // device address of vx_scratch in this context's GEMV module (vx_gemv_q_noalloc)
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
-    // activation workspace of vx_gemv_q at B >= 2 (grown on demand)
-    std::mutex ws_mu;
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
+    // Nothing here changes after vx_init: buffers a call needs beyond its
+    // operands are the caller's (vx_gemv_q_ws) or the module's scratch.
 };
 
 namespace vx {
@@ -743,36 +740,13 @@ static int run_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const 
     return launch_gemv_xq(ctx, stream, cy, w, q);
 }
 
-// The context's activation workspace, at least `bytes` large.
-static int workspace(vx_ctx ctx, vx_stream stream, size_t bytes, void** out) {
-    std::lock_guard<std::mutex> lock(ctx->ws_mu);
-    if (ctx->ws_bytes < bytes) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return fail(VX_ERR_UNSUPPORTED,
-                        "vx_gemv_q: the activation workspace must grow, which cannot happen during stream capture "
-                        "(make one call of this size before capturing, or use vx_gemv_q_noalloc)");
-        if (ctx->ws) {
-            hipError_t e = hipDeviceSynchronize();  // the old buffer may still be in use
-            if (e != hipSuccess) return fail_hip(e, "hipDeviceSynchronize");
-            (void)hipFree(ctx->ws);
-            ctx->ws = nullptr;
-            ctx->ws_bytes = 0;
-        }
-        const size_t sz = (bytes + (1u << 20) - 1u) & ~(size_t)((1u << 20) - 1u);  // whole MiB
-        hipError_t e = hipMalloc(&ctx->ws, sz);
-        if (e != hipSuccess) {
-            ctx->ws = nullptr;
-            return fail_hip(e, "hipMalloc (activation workspace)");
-        }
-        ctx->ws_bytes = sz;
-    }
-    *out = ctx->ws;
-    return VX_OK;
-}
+// Where the batched GEMV's activation split may go: nowhere (vx_gemv_q /
+// _ex), a caller's workspace (vx_gemv_q_ws) or the module scratch
+// (vx_gemv_q_noalloc).
+enum SplitMem { SPLIT_NONE = 0, SPLIT_WS = 1, SPLIT_SCRATCH = 2 };
 
 static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
-                      uint32_t flags, bool noalloc = false) {
+                      uint32_t flags, SplitMem mem = SPLIT_NONE, void* ws = nullptr, uint64_t ws_bytes = 0) {
     clear_error();
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
     uint32_t qk, bb;
@@ -813,34 +787,47 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     const bool fast = K > 0 && K % 64 == 0 && ((uintptr_t)w->base & 3u) == 0 && w->row_stride_bytes % 4 == 0;
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
     // x as two int8 levels per 32-block (the default) or exact f32 (VX_GEMV_X_F32)
-    const bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
-    const bool force_simt = x_f32;
-    if (B >= 2 && !force_simt && xq_layout_ok(w) && xq_fused_ok(w, cx, B)) {
+    bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
+    if (B >= 2 && !x_f32 && xq_layout_ok(w) && xq_fused_ok(w, cx, B)) {
         // the matrix-core GEMV splitting x itself: one launch per 16 columns,
         // W streamed once per launch, no workspace
         return launch_gemv_xq(ctx, stream, cy, w, nullptr, &cx, B);
     }
-    if (B >= 2 && !force_simt && xq_layout_ok(w)) {
-        // split x once into the context's workspace, then the matrix-core
-        // GEMV on the split (W streamed once per 16 columns)
+    if (B >= 2 && !x_f32 && xq_layout_ok(w)) {
+        // split x once into memory (the caller's workspace or the module's
+        // scratch), then the matrix-core GEMV on the split (W streamed once
+        // per 16 columns)
         vx_xq q{nullptr, K, B};
         uint64_t nb;
         if ((s = xq_size(K, B, &nb))) return s;
-        if (noalloc) {
+        static thread_local std::string m;
+        if (mem == SPLIT_SCRATCH) {
             // the module's scratch array: no allocation, a fixed maximum
             if (nb > ctx->scratch_bytes) {
-                static thread_local std::string m;
                 m = "vx_gemv_q_noalloc: the split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) +
                     "] needs " + std::to_string(nb) + " bytes, more than the " + std::to_string(ctx->scratch_bytes) +
                     "-byte scratch (ceil(K/256) * B * 512 + (K/32) * B * 8 must not exceed it)";
                 return fail(VX_ERR_UNSUPPORTED, m.c_str());
             }
             q.base = ctx->scratch;
-        } else if ((s = workspace(ctx, stream, (size_t)nb, &q.base))) {
-            return s;
+        } else if (mem == SPLIT_WS && ws) {
+            if (ws_bytes < nb) {
+                m = "vx_gemv_q_ws: the split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) + "] needs " +
+                    std::to_string(nb) + " bytes of workspace, " + std::to_string(ws_bytes) + " given";
+                return fail(VX_ERR_INVALID, m.c_str());
+            }
+            q.base = ws;
+        } else if (flags & VX_GEMV_X_INT8) {
+            m = "the int8 split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) + "] at this shape needs " +
+                std::to_string(nb) + " bytes of device memory: pass a workspace (vx_gemv_q_ws)";
+            return fail(VX_ERR_UNSUPPORTED, m.c_str());
         }
-        if ((s = launch_quantize_x(ctx, stream, &q, cx))) return s;
-        return launch_gemv_xq(ctx, stream, cy, w, &q);
+        if (q.base) {
+            if ((s = launch_quantize_x(ctx, stream, &q, cx))) return s;
+            return launch_gemv_xq(ctx, stream, cy, w, &q);
+        }
+        // no memory for the split: exact f32 x (the VX_GEMV_X_F32 kernels)
+        x_f32 = true;
     }
     // batch-1 kernel: the persistent one, or the per-row-group one when x
     // does not fit the persistent kernel's LDS (K > 16384); int8 x unless
@@ -929,6 +916,31 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         b0 += NB;
     }
     return VX_OK;
+}
+
+// Read probe: vx_gemv_p1i's loads of W alone (measurement).
+static int run_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w, float* y) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    uint32_t qk, bb;
+    int s = check_qweight(w, &qk, &bb);
+    if (s) return s;
+    if (w->rows && !y) return fail(VX_ERR_INVALID, "null y");
+    if (!xq_layout_ok(w))
+        return fail(VX_ERR_UNSUPPORTED, "read probe needs K a multiple of 64 and 4-byte aligned weight rows");
+    if (w->rows == 0) return VX_OK;
+    DeviceGuard guard(ctx->device);
+    vx_gemv_args a{};
+    a.w = (const uint8_t*)w->base;
+    a.row_stride = w->row_stride_bytes;
+    a.y = y;
+    a.ys_m = 1;
+    a.M = w->rows;
+    a.K = w->cols;
+    a.nunits = w->cols / 64u;
+    const int k = q_index(w->qtype) == 0 ? K_vx_read_probe_q4_0 : q_index(w->qtype) == 1 ? K_vx_read_probe_q8_0
+                                                                                         : K_vx_read_probe_q4_k;
+    return launch(ctx, k, dim3((uint32_t)ctx->num_cus), dim3(1024u), 0, stream, a);
 }
 
 // ------------------------------------------------------------ contiguous
@@ -1105,10 +1117,6 @@ int vx_destroy(vx_ctx ctx) {
     vx::clear_error();
     if (!ctx) return VX_OK;
     vx::DeviceGuard guard(ctx->device);
-    if (ctx->ws) {
-        (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->ws);
-    }
     for (hipModule_t m : ctx->mods)
         if (m) (void)hipModuleUnload(m);
     delete ctx;
@@ -1161,6 +1169,26 @@ int vx_gemv_q_ex(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
     return vx::run_gemv_q(ctx, stream, y, w, x, flags);
 }
 
+int vx_gemv_q_ws(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweight* w, const vx_cview* x,
+                 uint32_t flags, void* workspace, uint64_t workspace_bytes) {
+    if (flags & ~(uint32_t)(VX_GEMV_X_INT8 | VX_GEMV_X_F32)) return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_ws flags");
+    if ((flags & VX_GEMV_X_INT8) && (flags & VX_GEMV_X_F32))
+        return vx::fail(VX_ERR_INVALID, "VX_GEMV_X_INT8 and VX_GEMV_X_F32 are exclusive");
+    if (((uintptr_t)workspace & 15u) != 0) return vx::fail(VX_ERR_INVALID, "workspace is not 16-byte aligned");
+    return vx::run_gemv_q(ctx, stream, y, w, x, flags, vx::SPLIT_WS, workspace, workspace_bytes);
+}
+
+int vx_gemv_q_ws_size(uint32_t qtype, uint32_t K, uint32_t B, uint32_t flags, uint64_t* bytes) {
+    vx::clear_error();
+    if (!bytes) return vx::fail(VX_ERR_INVALID, "null bytes");
+    uint32_t qk, bb;
+    int s = vx::qinfo(qtype, &qk, &bb);
+    if (s) return s;
+    *bytes = 0;
+    if (B < 2 || (flags & VX_GEMV_X_F32) || K % 64u != 0u) return VX_OK;
+    return vx::xq_size(K, B, bytes);
+}
+
 int vx_xq_size(uint32_t K, uint32_t B, uint64_t* bytes) {
     vx::clear_error();
     if (!bytes) return vx::fail(VX_ERR_INVALID, "null bytes");
@@ -1175,6 +1203,10 @@ int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
     return vx::run_gemv_q_xq(ctx, stream, y, w, x);
 }
 
+int vx_gemv_q_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w, float* y) {
+    return vx::run_read_probe(ctx, stream, w, y);
+}
+
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     return vx::run_dequant(ctx, stream, out, w);
 }
@@ -1185,7 +1217,7 @@ int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
         return vx::fail(VX_ERR_INVALID, "unknown vx_gemv_q_noalloc flags");
     if ((flags & VX_GEMV_X_INT8) && (flags & VX_GEMV_X_F32))
         return vx::fail(VX_ERR_INVALID, "VX_GEMV_X_INT8 and VX_GEMV_X_F32 are exclusive");
-    return vx::run_gemv_q(ctx, stream, y, w, x, flags, true);
+    return vx::run_gemv_q(ctx, stream, y, w, x, flags, vx::SPLIT_SCRATCH);
 }
 
 int vx_quantize(vx_ctx ctx, vx_stream stream, const vx_qweight* out, const vx_cview* x) {
