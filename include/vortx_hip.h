@@ -332,7 +332,7 @@ int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y,
 /* Measurement only, no counterpart in the reference: the loads of the
  * batch-1 GEMV (vx_gemv_q at B = 1) with nothing else — the same grid, row
  * order and per-lane 64-weight units, every item of a round of four in
- * flight, no x, no barrier, no arithmetic. Reads every byte of W once and
+ * flight (none past a wave's last row), no x, no barrier, no arithmetic. Reads every byte of W once and
  * writes one word per row to y[0..M) (contents unspecified). Its time is
  * the ceiling of what that access pattern streams in one launch. Needs K a
  * multiple of 64 and 4-byte aligned rows (else VX_ERR_UNSUPPORTED). */

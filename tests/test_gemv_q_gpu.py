@@ -339,9 +339,13 @@ def test_gemv_without_workspace(qgemv, qtype):
     the f32 kernels' 1e-5), or, asked for the int8 split explicitly, fail
     with VX_ERR_UNSUPPORTED and launch nothing."""
     M = 300
-    # (K, B, fused): one item per wave and <= 8 columns fuse; 16 columns
-    # (two column groups) or K past 4096 (several items) need the split
-    for K, B, fused in ((4096, 4, True), (2048, 8, True), (4096, 16, False), (8192, 3, False)):
+    # (K, B, fused): one item per wave (up to 16 columns), two items with up
+    # to 8 columns or three with up to 4 fuse; three items with 8 columns,
+    # several passes (K past 16 waves x items) or more than 16 columns need
+    # the split in memory
+    big = 12288 if qtype == vx.VX_Q4_K else 11008
+    for K, B, fused in ((4096, 4, True), (2048, 8, True), (4096, 16, True), (8192, 3, True), (big, 8, False),
+                        (4096, 20, False)):
         note(f"gemv no-workspace {QN[qtype]} K={K} B={B}")
         w = torch.from_numpy(S.quant_weights(qtype, M, K, seed=42 + K).numpy()).to(DEV)
         qw = vx.QWeight(w, qtype, M, K)
@@ -384,7 +388,7 @@ def test_gemv_two_streams_own_workspaces(qgemv):
     """One context, two streams, each with its own workspace, running
     interleaved batched GEMVs that need the split in memory: every result
     equals the serial run bit for bit (the context holds no per-call state)."""
-    cases = [(vx.VX_Q4_K, 2048, 4096, 16), (vx.VX_Q4_0, 1024, 11008, 8), (vx.VX_Q8_0, 512, 8192, 12)]
+    cases = [(vx.VX_Q4_K, 2048, 12288, 16), (vx.VX_Q4_0, 1024, 11008, 8), (vx.VX_Q8_0, 512, 8192, 12)]
     data = []
     for i, (qt, M, K, B) in enumerate(cases):
         qw = vx.QWeight(S.quant_weights(qt, M, K, seed=50 + i, device=DEV), qt, M, K)

@@ -15,8 +15,10 @@ DEV = torch.device("cuda:0")
 @pytest.mark.parametrize("B,use_ws", [(1, False), (4, False), (16, False), (16, True), (5, True)])
 def test_gemv_graph_replay_matches_eager(qgemv, B, use_ws):
     """use_ws: one caller workspace shared by the captured launches (one
-    stream, so in order); at B = 16 and at K = 8192 the split goes there."""
-    M, K, n = 300, 8192 if B == 5 else 1024, 6
+    stream, so in order); at these shapes (several passes at B = 16, three
+    items with 5 columns) the split goes there."""
+    M, n = 300, 6
+    K = (12288 if B == 16 else 11008) if use_ws else 1024
     note(f"graph replay gemv B={B} workspace={use_ws}")
     ws = [S.quant_weights(vx.VX_Q4_K if B == 16 else vx.VX_Q4_0, M, K, seed=i, device=DEV) for i in range(n)]
     qt = vx.VX_Q4_K if B == 16 else vx.VX_Q4_0

@@ -192,13 +192,14 @@ def test_xq_errors(qgemv):
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 @pytest.mark.parametrize("M,K,B", [(300, 4096, 8), (131, 4096, 2), (257, 832, 5), (64, 1536, 16), (45, 8192, 3),
                                    (70, 11008, 4), (33, 4096, 13), (100, 2048, 21), (16, 4096, 9),
-                                   (300, 4096, 4), (257, 832, 3), (40, 2048, 4)])
+                                   (300, 4096, 4), (257, 832, 3), (40, 2048, 4), (200, 8192, 7), (257, 12288, 4),
+                                   (96, 4096, 16)])
 def test_fused_split_equals_split_then_gemv(qgemv, qtype, M, K, B):
     """vx_gemv_q with x stored [B, K] (stride 1 along K) splits x inside the
     GEMV kernels (one launch); stored [K, B] it runs vx_quantize_x into the
-    caller's workspace, then the GEMV on the split. Same bytes of x, same kernels otherwise: y is equal bit
-    for bit. (The host fuses only one item and one group of 8 columns per
-    wave, B <= 8 with K <= 4096; the other shapes check that both storages
+    caller's workspace, then the GEMV on the split. Same bytes of x, same
+    kernels otherwise: y is equal bit for bit. (The host fuses one pass with one item per wave at B <= 16, two
+    at B <= 8 or three at B <= 4; the other shapes check that both storages
     take the split path and agree.)"""
     if K % O.QTYPE_INFO[qtype][0]:
         pytest.skip("K not a multiple of the block size")

@@ -2,7 +2,8 @@
 vx_gemv_q_ws (the same routes with a caller workspace), both called through
 the C ABI: the same kernels on the same inputs, so y must be identical bit
 for bit and within tolerance of the oracle. The cases take the route that
-splits x into memory (several items per wave, or more than 8 columns), so
+splits x into memory (the shapes whose split does not fit the GEMV kernel's
+registers), so
 every call goes through the module's scratch array; they run largest first
 after a call that fills almost all of the scratch with other data, so a
 call that read stale scratch contents would show. A split that does not fit
@@ -46,8 +47,9 @@ def test_noalloc_matches_gemv_q_ws_decreasing(qgemv, flags):
     xf = S.activations(Bf, Kf, seed=6, device=DEV) * 100.0
     yf = torch.empty((Bf, Mf), device=DEV)
     assert _gemv(L.vx_gemv_q_noalloc, qgemv, yf.t(), wf, xf.t()) == 0
-    # largest split first: 198 KB, 147 KB, 74 KB
-    cases = [(vx.VX_Q4_0, 4096, 11008, 8), (vx.VX_Q4_K, 14336, 4096, 16), (vx.VX_Q8_0, 512, 8192, 4)]
+    # shapes the GEMV cannot split x for itself (several passes, or three
+    # items with 8 columns), largest split first: 442 KB, 198 KB, 124 KB
+    cases = [(vx.VX_Q4_K, 2048, 12288, 16), (vx.VX_Q4_0, 4096, 11008, 8), (vx.VX_Q8_0, 512, 11008, 5)]
     for qtype, M, K, B in cases:
         note(f"noalloc {qtype} {M}x{K} B={B} flags={flags}")
         w = vx.QWeight(S.quant_weights(qtype, M, K, seed=M, device=DEV), qtype, M, K)

@@ -706,9 +706,10 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
 // else. Same grid, wave-major row numbering and per-lane units; no x, no
 // barrier, no arithmetic; every item of a round of P in flight before any is
 // used (an empty asm statement consumes each loaded word, so the loads stay
-// and their waits are real). Lane 0 writes its XOR of the row's words to y:
-// the bytes of the GEMV without x. Its time is the ceiling of what the
-// GEMV's access pattern can stream in one launch.
+// and their waits are real), nothing loaded past the wave's last item.
+// Lane 0 writes its XOR of the row's words to y: the bytes of the GEMV
+// without x. Its time is the ceiling of what the GEMV's access pattern can
+// stream in one launch.
 template <int QT, int P>
 __device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
@@ -724,13 +725,16 @@ __device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a) {
         uint32_t wr[P][NW];
 #pragma unroll
         for (int j = 0; j < P; ++j) {
-            // past the wave's last item every lane reads the matrix's first
-            // unit (one cache line), as the GEMV's ring does
-            const bool past = it0 + (uint32_t)j >= nitems;  // wave-uniform
-            const uint32_t it = min(it0 + (uint32_t)j, nitems - 1u);
-            const uint32_t ri = it / npass, p = it - ri * npass;
-            vx_load_unit<QT, true>(past ? a.w : a.w + (uint64_t)(gw + ri * nwv) * a.row_stride,
-                                   past ? 0u : min(64u * p + lane, nunits - 1u), wr[j]);
+            // nothing is loaded past the wave's last item (wave-uniform)
+            const uint32_t it = it0 + (uint32_t)j;
+            if (it < nitems) {
+                const uint32_t ri = it / npass, p = it - ri * npass;
+                vx_load_unit<QT, true>(a.w + (uint64_t)(gw + ri * nwv) * a.row_stride, min(64u * p + lane, nunits - 1u),
+                                       wr[j]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < NW; ++q) wr[j][q] = 0u;
+            }
         }
 #pragma unroll
         for (int j = 0; j < P; ++j) {
@@ -1548,27 +1552,42 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #define VX_GEMV_XQ1(QT, QN, NCG, XI, RD)                       \
     VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, false, , false)     \
     VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, false, _st, false)
-// the fused split only where each wave splits one chunk (one item, one
-// column group): further chunks cost more than the launch they save
+// _fx: x split in the kernel, for the one-pass shapes whose split fits the
+// registers: one item per wave (any B <= 16), or 2-3 items with B <= 4
+// (_fx4: each lane splits half the blocks) or 2 items with B <= 8
+#define VX_GEMV_XQF(QT, QN, NCG, XI, RD)                                           \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, false, true, _fx, false)                \
+    VX_GEMV_XQ(QT, QN, NCG, XI, RD, false, true, true, _st_fx, false)
+#define VX_GEMV_XQF4(QT, QN, XI, RD)                                              \
+    VX_GEMV_XQ(QT, QN, 1, XI, RD, false, false, true, _fx4, true)                 \
+    VX_GEMV_XQ(QT, QN, 1, XI, RD, false, true, true, _st_fx4, true)
 #define VX_GEMV_XQ1F(QT, QN, RD)                               \
     VX_GEMV_XQ1(QT, QN, 1, 1, RD)                              \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx, false)      \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx, false)    \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, false, true, _fx4, true)      \
-    VX_GEMV_XQ(QT, QN, 1, 1, RD, false, true, true, _st_fx4, true)
+    VX_GEMV_XQF(QT, QN, 1, 1, RD)                              \
+    VX_GEMV_XQF4(QT, QN, 1, RD)
 VX_GEMV_XQ1F(VX_Q4_0, q4_0, 4)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
+VX_GEMV_XQF(VX_Q4_0, q4_0, 1, 2, 1)
+VX_GEMV_XQF4(VX_Q4_0, q4_0, 2, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 3, 1)
+VX_GEMV_XQF4(VX_Q4_0, q4_0, 3, 1)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 2, 1, 3)
+VX_GEMV_XQF(VX_Q4_0, q4_0, 2, 1, 3)
 VX_GEMV_XQ(VX_Q4_0, q4_0, 1, 3, 1, true, false, false, _mp, false)
 VX_GEMV_XQ(VX_Q4_0, q4_0, 2, 1, 1, true, false, false, _mp, false)
 VX_GEMV_XQ1F(VX_Q8_0, q8_0, 2)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 1, 2, 1)
+VX_GEMV_XQF(VX_Q8_0, q8_0, 1, 2, 1)
+VX_GEMV_XQF4(VX_Q8_0, q8_0, 2, 1)
 VX_GEMV_XQ1(VX_Q8_0, q8_0, 2, 1, 2)
+VX_GEMV_XQF(VX_Q8_0, q8_0, 2, 1, 2)
 VX_GEMV_XQ(VX_Q8_0, q8_0, 1, 2, 1, true, false, false, _mp, false)
 VX_GEMV_XQ(VX_Q8_0, q8_0, 2, 1, 1, true, false, false, _mp, false)
 VX_GEMV_XQ1F(VX_Q4_K, q4_k, 3)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 1, 2, 1)
+VX_GEMV_XQF(VX_Q4_K, q4_k, 1, 2, 1)
+VX_GEMV_XQF4(VX_Q4_K, q4_k, 2, 1)
 VX_GEMV_XQ1(VX_Q4_K, q4_k, 2, 1, 2)
+VX_GEMV_XQF(VX_Q4_K, q4_k, 2, 1, 2)
 VX_GEMV_XQ(VX_Q4_K, q4_k, 1, 2, 1, true, false, false, _mp, false)
 VX_GEMV_XQ(VX_Q4_K, q4_k, 2, 1, 1, true, false, false, _mp, false)

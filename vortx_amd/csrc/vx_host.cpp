@@ -602,11 +602,20 @@ static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx, bo
 #define VX_XQK(N) (st ? K_vx_gemv_xq_##N##_st : K_vx_gemv_xq_##N)
 #define VX_XQF(N) (fh ? (st ? K_vx_gemv_xq_##N##_st_fx4 : K_vx_gemv_xq_##N##_fx4) \
                       : (st ? K_vx_gemv_xq_##N##_st_fx : K_vx_gemv_xq_##N##_fx))
-    if (fx) {  // one item, one column group (xq_fused_ok)
-        const int q = q_index(qt);
-        if (q == 0) return VX_XQF(q4_0_c1_x1);
-        if (q == 1) return VX_XQF(q8_0_c1_x1);
-        return VX_XQF(q4_k_c1_x1);
+#define VX_XQF2(N) (st ? K_vx_gemv_xq_##N##_st_fx : K_vx_gemv_xq_##N##_fx)
+#define VX_XQF4(N) (st ? K_vx_gemv_xq_##N##_st_fx4 : K_vx_gemv_xq_##N##_fx4)
+    if (fx) {  // one pass; the shapes xq_fused_shape admits
+        switch (q_index(qt)) {
+        case 0:
+            if (ncg == 2) return VX_XQF2(q4_0_c2_x1);
+            return xi == 1 ? VX_XQF(q4_0_c1_x1) : xi == 2 ? VX_XQF(q4_0_c1_x2) : VX_XQF4(q4_0_c1_x3);
+        case 1:
+            if (ncg == 2) return VX_XQF2(q8_0_c2_x1);
+            return xi == 1 ? VX_XQF(q8_0_c1_x1) : VX_XQF(q8_0_c1_x2);
+        default:
+            if (ncg == 2) return VX_XQF2(q4_k_c2_x1);
+            return xi == 1 ? VX_XQF(q4_k_c1_x1) : VX_XQF(q4_k_c1_x2);
+        }
     }
     switch (q_index(qt)) {
     case 0:
@@ -624,6 +633,8 @@ static int xq_kernel(uint32_t qt, int ncg, int xi, bool mp, bool st, bool fx, bo
     }
 #undef VX_XQK
 #undef VX_XQF
+#undef VX_XQF2
+#undef VX_XQF4
 }
 
 // Items per wave and pass for a launch of b columns: the x levels of XI items
@@ -636,6 +647,18 @@ static int xq_items(uint32_t qt, uint32_t K, uint32_t b, bool* mp) {
     int xi = (int)((ipr + 15u) / 16u);
     *mp = xi > xmax;
     return *mp ? xmax : xi;
+}
+
+// Whether a launch of b (<= 16) columns has a kernel that splits x itself:
+// one pass, and the split of the wave's slice fits the registers: one item
+// per wave (one or two groups of 8 columns), two items with <= 8 columns, or
+// three items with <= 4 columns (each lane splitting half the blocks).
+static bool xq_fused_shape(uint32_t qt, uint32_t K, uint32_t b) {
+    bool mp;
+    const int xi = xq_items(qt, K, b, &mp);
+    if (mp || b > 16u) return false;
+    if (b > 8u) return xi == 1;
+    return xi <= 2 || b <= 4u;
 }
 
 // y [.., M, B] (canonical) = W x, x given by its split q (q->K == K, q->B ==
@@ -671,8 +694,8 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
         const int ncg = a.B > 8u ? 2 : 1;
         bool mp;
         const int xi = xq_items(w->qtype, K, a.B, &mp);
-        if (fx && (mp || xi != 1 || ncg != 1))
-            return fail(VX_ERR_UNSUPPORTED, "internal: the fused split needs one pass of one item and <= 8 columns");
+        if (fx && !xq_fused_shape(w->qtype, K, a.B))
+            return fail(VX_ERR_UNSUPPORTED, "internal: no kernel splits x itself at this shape");
         a.npass = (a.ipr + 16u * (uint32_t)xi - 1u) / (16u * (uint32_t)xi);
         // 64 KB of parked partial sums + each of the 16 waves' scales (+ the
         // fused split's per-wave tables)
@@ -691,17 +714,15 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
 }
 
 // The batched GEMV splits x inside its kernels (one launch, no workspace)
-// when x has stride 1 along K with 16-byte aligned columns and each wave
-// splits one chunk (one item, one group of 8 columns: B <= 8, K <= 4096).
-// Each further chunk adds its own load latency and arithmetic before the
-// weight stream starts, which costs more than the second launch saves
-// (measured: Q4_0 11008x4096 B = 8 13.0 -> 11.7 us per step, but 4096x11008
-// B = 8 (3 items) 15.8 -> 19.9 us and Q4_K 14336x4096 B = 16 (2 column
-// groups) 18.3 -> 21.0 us).
+// when x has stride 1 along K with 16-byte aligned columns, B <= 16 and the
+// shape has a fused kernel (xq_fused_shape). Measured per step against the
+// split-then-GEMV route (graph replay): Q4_0 11008x4096 B = 8 13.0 -> 11.7
+// us, 4096x11008 B = 4 (three items, half the blocks per lane) 13.6 -> 11.6
+// us, Q4_K 32000x4096 B = 16 (two column groups) 29.6 -> 28.2 us, 14336x4096
+// B = 16 18.2 -> 18.7 us (even: kept fused, it needs no workspace).
 static bool xq_fused_ok(const vx_qweight* w, const Canon& cx, uint32_t B) {
-    if (B > 8u || cx.l.stride[2] != 1 || !aligned16(cx.ptr) || (B > 1u && cx.l.stride[3] % 4 != 0)) return false;
-    bool mp;
-    return xq_items(w->qtype, w->cols, B, &mp) == 1 && !mp;
+    if (B > 16u || cx.l.stride[2] != 1 || !aligned16(cx.ptr) || (B > 1u && cx.l.stride[3] % 4 != 0)) return false;
+    return xq_fused_shape(w->qtype, w->cols, B);
 }
 
 static bool xq_layout_ok(const vx_qweight* w) {
@@ -788,6 +809,18 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
     const size_t budget = ctx->lds_per_block < 160u * 1024u ? ctx->lds_per_block : 160u * 1024u;
     // x as two int8 levels per 32-block (the default) or exact f32 (VX_GEMV_X_F32)
     bool x_f32 = (flags & VX_GEMV_X_F32) != 0;
+    if (mem == SPLIT_WS && ws && B >= 2 && !x_f32 && K % 64u == 0u) {
+        // a caller workspace is checked against what the call may use
+        // (vx_gemv_q_ws_size), whichever route the shape then takes
+        uint64_t nb;
+        if ((s = xq_size(K, B, &nb))) return s;
+        if (ws_bytes < nb) {
+            static thread_local std::string m;
+            m = "vx_gemv_q_ws: x [K=" + std::to_string(K) + ", B=" + std::to_string(B) + "] needs " +
+                std::to_string(nb) + " bytes of workspace, " + std::to_string(ws_bytes) + " given";
+            return fail(VX_ERR_INVALID, m.c_str());
+        }
+    }
     if (B >= 2 && !x_f32 && xq_layout_ok(w) && xq_fused_ok(w, cx, B)) {
         // the matrix-core GEMV splitting x itself: one launch per 16 columns,
         // W streamed once per launch, no workspace
@@ -811,12 +844,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             }
             q.base = ctx->scratch;
         } else if (mem == SPLIT_WS && ws) {
-            if (ws_bytes < nb) {
-                m = "vx_gemv_q_ws: the split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) + "] needs " +
-                    std::to_string(nb) + " bytes of workspace, " + std::to_string(ws_bytes) + " given";
-                return fail(VX_ERR_INVALID, m.c_str());
-            }
-            q.base = ws;
+            q.base = ws;  // its size was checked above
         } else if (flags & VX_GEMV_X_INT8) {
             m = "the int8 split of x [K=" + std::to_string(K) + ", B=" + std::to_string(B) + "] at this shape needs " +
                 std::to_string(nb) + " bytes of device memory: pass a workspace (vx_gemv_q_ws)";
