@@ -277,8 +277,9 @@ int vx_gemv_q_ws_size(uint32_t qtype, uint32_t K, uint32_t B, uint32_t flags,
  * the order of a Q4_0 block's nibbles. Layout in one device buffer, with
  * NI = ceil(K / 256) items of 8 blocks:
  *   levels int8 at byte 0: level L of column b, block j, position p at
- *     ((j/8 B + b) 2 + L) 256 + (p/8) 64 + (j%8) 8 + p%8 (the 8 bytes one
- *     matrix-core lane takes from each of an item's 8 blocks lie together;
+ *     (j/8) B 512 + ((j%8)/2) B 128 + (p/8) B 32 + b 32 + L 16 + (j%2) 8
+ *     + p%8 (the 16 bytes one matrix-core lane takes from a block pair lie
+ *     together, and the lanes of one load read consecutive 16-byte pieces;
  *     blocks past K/32 in the last item are unused);
  *   scales f32 [K/32][B][2] at byte NI B 512: {c2, S}, or {m + S, S}
  *     (non-finite) for a block holding a NaN or inf.

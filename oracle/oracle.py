@@ -284,11 +284,12 @@ def xq_decode_f64(levels: np.ndarray, scales: np.ndarray) -> np.ndarray:
 
 def xq_device_levels(levels: np.ndarray) -> np.ndarray:
     """The oracle's levels [K/32, B, 2, 32] (positions in XQ_POS order) in the
-    library's device layout [ceil(K/256), B, 2, 4, 8, 8] (item, column, level,
-    position group p/8, block of the item, byte p%8; blocks past K/32 zero)."""
+    library's device layout [ceil(K/256), 4, 4, B, 2, 2, 8] (item, block pair
+    (j%8)/2, position group p/8, column, level, block parity j%2, byte p%8;
+    blocks past K/32 zero)."""
     nblk, B = levels.shape[:2]
     ni = -(-nblk // 8)
     pad = np.zeros((ni * 8, B, 2, 32), dtype=np.int8)
     pad[:nblk] = levels
-    v = pad.reshape(ni, 8, B, 2, 4, 8)          # item, block-of-item, col, level, group, byte
-    return np.ascontiguousarray(v.transpose(0, 2, 3, 4, 1, 5))
+    v = pad.reshape(ni, 4, 2, B, 2, 4, 8)       # item, pair, parity, col, level, group, byte
+    return np.ascontiguousarray(v.transpose(0, 1, 5, 3, 4, 2, 6))

@@ -195,3 +195,27 @@ def test_clamps_never_act():
     got = lv.reshape(-1, 2, 32)
     pos = O.XQ_POS
     assert np.array_equal(got[:, 0, pos], q1c) and np.array_equal(got[:, 1, pos], np.rint(t2c))
+
+
+def test_device_layout_round_trip_and_coalescing():
+    """O.xq_device_levels places level L of column b, block j, position p at
+    (j/8) B 512 + ((j%8)/2) B 128 + (p/8) B 32 + b 32 + L 16 + (j%2) 8 + p%8
+    (the header's formula), and the 16 bytes a matrix-core lane (b, L, group
+    g) loads for a block pair are contiguous, with consecutive (b, L) lanes of
+    one load 16 bytes apart."""
+    rng = np.random.default_rng(3)
+    K, B = 800, 5                      # 25 blocks: a partial last item
+    lv = rng.integers(-127, 128, (K // 32, B, 2, 32), dtype=np.int8)
+    dev = O.xq_device_levels(lv).reshape(-1)
+    assert dev.size == (-(-K // 256)) * B * 512
+    for j in (0, 1, 7, 8, 13, 24):
+        for b in range(B):
+            for L in range(2):
+                for p in (0, 5, 8, 17, 31):
+                    off = (j // 8) * B * 512 + ((j % 8) // 2) * B * 128 + (p // 8) * B * 32 + b * 32 + L * 16 + \
+                        (j % 2) * 8 + p % 8
+                    assert dev[off] == lv[j, b, L, p], (j, b, L, p)
+    # the inverse used by the GPU tests
+    d = dev.reshape(-1, 4, 4, B, 2, 2, 8)
+    back = d.transpose(0, 1, 5, 3, 4, 2, 6).reshape(-1, B, 2, 32)[:K // 32]
+    assert np.array_equal(back, lv)

@@ -29,11 +29,12 @@ XQ_GEMV_TOL = 2e-5
 
 
 def _logical_levels(q: vx.XQ) -> np.ndarray:
-    """Device-layout levels [ceil(K/256), B, 2, 4, 8, 8] -> [K/32, B, 2, 32]
+    """Device-layout levels [ceil(K/256), 4, 4, B, 2, 2, 8] (item, block pair,
+    position group, column, level, block parity, byte) -> [K/32, B, 2, 32]
     (the oracle's layout); O.xq_device_levels is the inverse."""
     d = q.levels().cpu().numpy()
-    ni, B = d.shape[:2]
-    lv = d.transpose(0, 4, 1, 2, 3, 5).reshape(ni * 8, B, 2, 32)
+    ni, B = d.shape[0], d.shape[3]
+    lv = d.transpose(0, 1, 5, 3, 4, 2, 6).reshape(ni * 8, B, 2, 32)
     return lv[:q.K // 32]
 
 

@@ -276,9 +276,9 @@ def xq_size(K: int, B: int) -> int:
 class XQ:
     """x [K, B] split into two int8 levels per 32-block (vx_xq): a uint8 GPU
     buffer of at least xq_size(K, B) bytes, 16-byte aligned. ``levels()``
-    views its level bytes in the device layout ([ceil(K/256), B, 2, 4, 8, 8]
-    int8: item, column, level, position group, block of the item, byte) and
-    ``scales()`` its [K/32, B, 2] f32 scales."""
+    views its level bytes in the device layout ([ceil(K/256), 4, 4, B, 2, 2, 8]
+    int8: item, block pair, position group, column, level, block parity,
+    byte) and ``scales()`` its [K/32, B, 2] f32 scales."""
     data: object
     K: int
     B: int
@@ -297,7 +297,7 @@ class XQ:
     def levels(self):
         import torch
         ni = (self.K + 255) // 256
-        return self.data[:ni * self.B * 512].view(torch.int8).view(ni, self.B, 2, 4, 8, 8)
+        return self.data[:ni * self.B * 512].view(torch.int8).view(ni, 4, 4, self.B, 2, 2, 8)
 
     def scales(self):
         import torch

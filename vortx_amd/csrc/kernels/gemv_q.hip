@@ -1221,14 +1221,15 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
 #pragma unroll
             for (int h = 0; h < NCG; ++h) {
                 // lane (i, g): level i % 2 of column 8 h + i / 2, the 8 bytes
-                // of position group g of each of the item's 8 blocks: 64
-                // contiguous bytes (vx_quantize_x's item-major layout)
+                // of position group g of each of the item's 8 blocks, 16
+                // bytes (blocks 2k, 2k + 1) per load k; the lanes of one load
+                // read consecutive 16-byte pieces (vx_quantize_x's layout)
                 const uint32_t col = 8u * (uint32_t)h + (n >> 1);
-                const uint8_t* lp = (const uint8_t*)a.levels +
-                                    (((uint64_t)min(item, ipr - 1u) * a.xcols + a.col0 + min(col, B - 1u)) * 2u +
-                                     (n & 1u)) * 256u + 64u * g;
-                const i64x2 v0 = *(const i64x2*)lp, v1 = *(const i64x2*)(lp + 16);
-                const i64x2 v2 = *(const i64x2*)(lp + 32), v3 = *(const i64x2*)(lp + 48);
+                const uint8_t* lp = (const uint8_t*)a.levels + (uint64_t)min(item, ipr - 1u) * a.xcols * 512u +
+                                    (uint64_t)(g * a.xcols + a.col0 + min(col, B - 1u)) * 32u + (n & 1u) * 16u;
+                const uint32_t ks = a.xcols * 128u;  // bytes from one block pair to the next
+                const i64x2 v0 = *(const i64x2*)lp, v1 = *(const i64x2*)(lp + ks);
+                const i64x2 v2 = *(const i64x2*)(lp + 2u * ks), v3 = *(const i64x2*)(lp + 3u * ks);
                 xa[j][0][h] = v0.x; xa[j][1][h] = v0.y; xa[j][2][h] = v1.x; xa[j][3][h] = v1.y;
                 xa[j][4][h] = v2.x; xa[j][5][h] = v2.y; xa[j][6][h] = v3.x; xa[j][7][h] = v3.y;
             }

@@ -414,9 +414,12 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_q4_k(vx_quant_args
 // 8 ((i - 16) / 4) + 4 + i % 4 (i >= 16): the order of a Q4_0 block's nibbles
 // (byte t holds elements t and t + 16), so a 32-bit word of Q4_0 nibbles and
 // 8 bytes of x levels line up for the int8 matrix cores. Levels are stored
-// [item = j / 8][b][level][g = position / 8][j % 8][position % 8]: the 8
-// bytes one matrix-core lane needs from each of an item's 8 blocks sit
-// together (64 bytes per lane). Scales [j][b] = {c2, S}; a block with a NaN
+// [item = j / 8][k = (j % 8) / 2][g = position / 8][b][level][j % 2]
+// [position % 8]: the 16 bytes one matrix-core lane (column b, level, group
+// g) needs from blocks 2k, 2k + 1 of an item sit together, and the lanes of
+// one load instruction (fixed k) read consecutive 16-byte pieces, so a
+// wave's load of 8 columns covers 1 KB contiguously (8 cache lines rather
+// than 64). Scales [j][b] = {c2, S}; a block with a NaN
 // or inf stores {m + S, S} and zero levels, so every output of its column
 // becomes non-finite.
 // Eight lanes per (j, b), lane t holding elements 4t..4t+3; every operation
@@ -449,12 +452,13 @@ extern "C" __global__ __launch_bounds__(256) void vx_quantize_x(vx_xq_args a) {
     vx_xq_levels4(v, sc.c1, sc.i1, sc.i2, fin, w1, w2);
     if (in) {
         // position dword dw (positions 4 dw..4 dw + 3, elements 4t..4t+3) of
-        // level L sits at ((item B + b) 2 + L) 256 + (dw / 2) 64 + (j % 8) 8 + (dw % 2) 4
+        // level L sits at item B 512 + ((j % 8) / 2) B 128 + (dw / 2) B 32 +
+        // b 32 + L 16 + (j % 2) 8 + (dw % 2) 4
         const uint32_t dw = t < 4u ? 2u * t : 2u * (t - 4u) + 1u;
-        uint8_t* base = (uint8_t*)a.levels + ((uint64_t)(j >> 3) * a.B + b) * 512u + (dw >> 1) * 64u + (j & 7u) * 8u +
-                        (dw & 1u) * 4u;
+        uint8_t* base = (uint8_t*)a.levels + (uint64_t)(j >> 3) * a.B * 512u + ((j & 7u) >> 1) * a.B * 128u +
+                        (dw >> 1) * a.B * 32u + b * 32u + (j & 1u) * 8u + (dw & 1u) * 4u;
         *(uint32_t*)base = w1;
-        *(uint32_t*)(base + 256u) = w2;
+        *(uint32_t*)(base + 16u) = w2;
         if (t == 0) *(float2*)(a.scales + 2u * grp) = float2{fin ? c2 : m + S, S};
     }
 }
