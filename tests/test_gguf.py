@@ -301,3 +301,15 @@ def test_view_rejects_misaligned_f32(tmp_path):
     assert f.tensor("b").offset == 2
     v = _ffi.VxCView()
     assert vx.lib().vx_gguf_view(f._h, f.index("b"), FAKE, C.byref(v)) == _ffi.VX_ERR_UNSUPPORTED
+
+
+def test_nul_in_key_or_tensor_name_is_rejected(tmp_path):
+    """Keys and tensor names are handed out NUL-terminated, so one holding a
+    NUL byte could not be found by its own name (the sanitized fuzzer found
+    such a file); the reader rejects it as malformed."""
+    good = W.build([("a.b", W.UINT32, 1)], [("t", [32], 0, bytes(128))])
+    assert vx.GGUFFile(_write(tmp_path, good)).header["n_kv"] == 1
+    bad_key = W.build([("a\0b", W.UINT32, 1)], [])
+    assert _status(_write(tmp_path, bad_key, "k.gguf")) == vx._ffi.VX_ERR_FORMAT
+    bad_name = W.build([], [("t\0u", [32], 0, bytes(128))])
+    assert _status(_write(tmp_path, bad_name, "n.gguf")) == vx._ffi.VX_ERR_FORMAT

@@ -230,6 +230,9 @@ int parse(vx_gguf_file* f) {
         Kv kv;
         if (!c.str(&s, &len)) return bad("metadata key runs past the end of the file");
         if (len == 0 || len > kMaxKeyLen) return bad("metadata key length out of range");
+        // keys are handed out NUL-terminated: an embedded NUL could never be
+        // looked up by name (the specification asks for ASCII keys)
+        if (std::memchr(s, 0, len)) return bad("metadata key holds a NUL byte");
         kv.key.assign((const char*)s, len);
         if (!c.u32(&kv.type)) return bad("metadata type runs past the end of the file");
         kv.elem_type = kv.type;
@@ -253,6 +256,7 @@ int parse(vx_gguf_file* f) {
     for (uint64_t i = 0; i < nt; ++i) {
         Tensor t;
         if (!c.str(&s, &len)) return bad("tensor name runs past the end of the file");
+        if (std::memchr(s, 0, len)) return bad("tensor name holds a NUL byte");
         t.name.assign((const char*)s, len);
         if (!c.u32(&t.n_dims)) return bad("tensor info runs past the end of the file");
         if (t.n_dims < 1 || t.n_dims > kMaxDims) return bad("tensor '" + t.name + "' has n_dims outside 1..4");
