@@ -600,7 +600,7 @@ def main() -> int:
     VERBOSE = args.verbose
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the hot path shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the hot path shards by output rows). Run with --gpus 1.", file=sys.stderr)
         return 2
 
     if args.cpu_baseline_only:
