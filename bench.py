@@ -162,14 +162,15 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     alg = M * S.row_bytes(qtype, K) + 4 * M if probe else gemv_bytes(qtype, M, K, B)
     r = {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
          "step_ms_events": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
-    # the library's route (xq_fused_shape in vx_host.cpp): the GEMV splits x
-    # itself (one launch) with one pass and one 256-weight item per wave (B <=
-    # 16), two with B <= 8 or three with B <= 4; otherwise the split goes to
-    # the workspace first (two launches)
+    # the library's route with a workspace (xq_fused_ok in vx_host.cpp): the
+    # GEMV splits x itself (one launch) with one pass and one 256-weight item
+    # per wave (B <= 16), two with B <= 8 or three with B <= 4, except two
+    # column groups below M = 24576; otherwise the split goes to the
+    # workspace first (two launches)
     ipr = (K // 64 + 3) // 4
     xmax = 1 if B > 8 else (3 if qtype == 2 else 2)
     xi = (ipr + 15) // 16
-    fused = 2 <= B <= 16 and xi <= xmax and (xi == 1 or (B <= 8 and xi == 2) or B <= 4)
+    fused = 2 <= B <= 16 and xi <= xmax and (xi == 1 or (B <= 8 and xi == 2) or B <= 4) and not (B > 8 and M < 24576)
     if B >= 2 and not x_f32 and not probe and not fused:
         q = vx.XQ.empty(K, B)
         g.quantize_x(q, xv)

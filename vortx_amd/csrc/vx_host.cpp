@@ -720,8 +720,14 @@ static int launch_gemv_xq(vx_ctx ctx, vx_stream stream, const Canon& cy, const v
 // us, 4096x11008 B = 4 (three items, half the blocks per lane) 13.6 -> 11.6
 // us, Q4_K 32000x4096 B = 16 (two column groups) 29.6 -> 28.2 us, 14336x4096
 // B = 16 18.2 -> 18.7 us (even: kept fused, it needs no workspace).
-static bool xq_fused_ok(const vx_qweight* w, const Canon& cx, uint32_t B) {
+// With memory for the split (have_mem), two column groups (B = 9..16) take
+// the split route below M = 24576: there every CU splitting all of x (16
+// columns, two chunks per wave) costs more than the second launch (measured,
+// graph-replayed: Q4_K 14336x4096 B = 16 fused 18.9 us, split 2.8 + GEMV
+// 14.4 us; 32000x4096 28.2 against 2.8 + 26.2 us).
+static bool xq_fused_ok(const vx_qweight* w, const Canon& cx, uint32_t B, bool have_mem = false) {
     if (B > 16u || cx.l.stride[2] != 1 || !aligned16(cx.ptr) || (B > 1u && cx.l.stride[3] % 4 != 0)) return false;
+    if (have_mem && B > 8u && w->rows < 24576u) return false;
     return xq_fused_shape(w->qtype, w->cols, B);
 }
 
@@ -821,7 +827,8 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             return fail(VX_ERR_INVALID, m.c_str());
         }
     }
-    if (B >= 2 && !x_f32 && xq_layout_ok(w) && xq_fused_ok(w, cx, B)) {
+    const bool have_mem = mem == SPLIT_SCRATCH || (mem == SPLIT_WS && ws);
+    if (B >= 2 && !x_f32 && xq_layout_ok(w) && xq_fused_ok(w, cx, B, have_mem)) {
         // the matrix-core GEMV splitting x itself: one launch per 16 columns,
         // W streamed once per launch, no workspace
         return launch_gemv_xq(ctx, stream, cy, w, nullptr, &cx, B);
