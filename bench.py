@@ -183,6 +183,22 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     return r
 
 
+def time_launch_floor(steps: int, warmup: int):
+    """An empty kernel on the batch-1 GEMV's grid (vx_launch_floor), captured
+    into a HIP graph and replayed as in time_gemv: the fixed cost of one
+    launch, which every step pays before any byte moves."""
+    import torch
+
+    import vortx_amd as vx
+
+    g = vx.QuantGemv(0)
+    for _ in range(warmup):
+        g.launch_floor()
+    torch.cuda.synchronize()
+    done, wall, ev = graph_time(lambda i, s: g.launch_floor(stream=s), steps)
+    return {"steps": done, "ms_per_step": wall * 1e3 / done, "step_ms_events": ev / done}
+
+
 def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
     """f32 GEMV y = A x (the GEMM op's N == 1 route, vx_gemv_f32): A [M, K]
     row-major f32 read once, so 4 M K + 4 K + 4 M algorithmic bytes per launch;
@@ -502,7 +518,7 @@ GEMMS = {  # key -> (M, N, K, transb, workload)
 }
 # every workload in run order (the keys --only selects from)
 KEYS = (["gemv_q4_0_11008x4096_b1", "gemv_q8_0_4096x4096_b1", "gemv_q4_0_11008x4096_b1_f32x",
-         "read_q4_0_11008x4096", "read_q8_0_4096x4096"] + list(GEMV_SECONDARY) +
+         "read_q4_0_11008x4096", "read_q8_0_4096x4096", "launch_floor"] + list(GEMV_SECONDARY) +
         ["split_x_11008_b8", "split_x_4096_b16", "gemv_f32_11008x4096", "gemv_f32_1552x4096",
          "gemv_f32_32768x4096"] + list(GEMMS) +
         ["gemm_f32_broadcast_8x1024", "gemm_sweep", "contiguous_t8192", "copy_8192", "copy_3104x1024",
@@ -530,6 +546,8 @@ def run_workloads(keys, steps: int, warmup: int) -> dict:
             r = time_gemv(2, 11008, 4096, 1, many, max(warmup, 50), k, probe=True)
         elif k == "read_q8_0_4096x4096":
             r = time_gemv(8, 4096, 4096, 1, many, max(warmup, 50), k, probe=True)
+        elif k == "launch_floor":
+            r = time_launch_floor(many, 50)
         elif k in GEMV_SECONDARY:
             qt, M, K, B, _ = GEMV_SECONDARY[k]
             r = time_gemv(qt, M, K, B, many, max(warmup, 50), k)
@@ -643,6 +661,7 @@ def main() -> int:
 
     q40 = R["gemv_q4_0_11008x4096_b1"]
     probe = R["read_q4_0_11008x4096"]
+    floor = R["launch_floor"]
     gg = R["gguf_upload"]
     line = {
         "metric": METRIC,
@@ -669,6 +688,11 @@ def main() -> int:
                                    "alone (no x, no arithmetic), 25.4 MB"),
                              gemv_over_probe=rnd(q40["step_ms_events"] / probe["step_ms_events"], 3)),
         "read_ceiling_q8_0": gline("read_q8_0_4096x4096", "vx_gemv_q_read_probe on Q8_0 4096x4096"),
+        # the fixed cost of one launch (empty kernel, same grid, graph-replayed),
+        # and the headline's bytes over its step time minus that cost
+        "launch_floor": {"us": rnd(floor["step_ms_events"] * 1e3, 3),
+                         "headline_GBps_above_floor": rnd(q40["alg_bytes"] / ((q40["step_ms_events"] -
+                                                                               floor["step_ms_events"]) * 1e-3) / 1e9)},
         "gemm_4096": dict(gline("gemm_f32_4096", GEMMS["gemm_f32_4096"][4], "TFLOP/s", "mfma"),
                           steps=GEMM_STEPS, warmup=GEMM_WARMUP,
                           cpu_baseline=cpu["gemm4096"] if cpu else None),

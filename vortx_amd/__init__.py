@@ -373,6 +373,11 @@ class QuantGemv(_Context):
         wc = w._c()
         check(lib().vx_gemv_q_read_probe(self._h, _stream(stream), C.byref(wc), y.data_ptr()))
 
+    def launch_floor(self, stream=None) -> None:
+        """One empty launch on the batch-1 GEMV's grid (vx_launch_floor,
+        measurement only): the fixed cost of a launch."""
+        check(lib().vx_launch_floor(self._h, _stream(stream)))
+
     def quantize(self, out: "QWeight", x, stream=None) -> None:
         """Write the blocks of ``out`` from the f32 [rows, cols] view ``x``
         (ggml's reference quantizers; see include/vortx_hip.h vx_quantize)."""

@@ -81,6 +81,7 @@ SIGNATURES = [
                                C.c_void_p, C.c_uint64]),
     ("vx_gemv_q_ws_size", C.c_int, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _P(C.c_uint64)]),
     ("vx_gemv_q_read_probe", C.c_int, [C.c_void_p, C.c_void_p, _P(VxQWeight), C.c_void_p]),
+    ("vx_launch_floor", C.c_int, [C.c_void_p, C.c_void_p]),
     ("vx_dequantize", C.c_int, [C.c_void_p, C.c_void_p, _P(VxMView), _P(VxQWeight)]),
     ("vx_xq_size", C.c_int, [C.c_uint32, C.c_uint32, _P(C.c_uint64)]),
     ("vx_quantize_x", C.c_int, [C.c_void_p, C.c_void_p, _P(VxXq), _P(VxCView)]),

@@ -170,7 +170,7 @@ __device__ __forceinline__ void vx_gemv_b1(const vx_gemv_args& a) {
 // (K <= 16384).
 #define VX_P_XF 4096u
 
-template <int QT, int P, int WGT, bool XV>
+template <int QT, int P, int WGT, bool XV, bool XM = false>
 __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr int XPT = (int)(VX_P_XF / WGT);
@@ -178,11 +178,13 @@ __device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
     // wave-uniform (scalar) so that the item loop runs on scalar branches
     // and the wait counts stay exact
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t nwv = gridDim.x * (WGT / 64u);
+    const uint32_t G = gridDim.x, nwv = G * (WGT / 64u);
     // waves interleaved over the CUs (wave-major), so the rows left over
     // after whole rounds of nwv spread evenly: at M = 11008 every CU gets 43
-    // rows (CU-major numbering gives 176 CUs 48 rows and 80 CUs 32)
-    const uint32_t gw = wave * gridDim.x + blockIdx.x;
+    // rows (CU-major numbering gives 176 CUs 48 rows and 80 CUs 32). XM:
+    // positions per XCD as in vx_gemv_p1i.
+    const uint32_t pb = (XM && (G & 7u) == 0u) ? (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const uint32_t gw = wave * G + pb;
     const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
     const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
     const uint32_t nitems = nrows * npass;
@@ -579,6 +581,78 @@ __device__ __forceinline__ void vx_split_store_b1(const vx_i8lds& L, uint32_t f,
     }
 }
 
+// Unsigned maximum over each aligned group of 8 lanes (DPP). Used on the
+// bits of |x|: for non-negative floats the integer order is the float order.
+__device__ __forceinline__ uint32_t vx_umax8(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+}
+
+// vx_split_store_b1 for N float4 per lane (f, f + stride, ...), the N
+// dependency chains interleaved step by step so their DPP reductions and
+// divisions overlap. The block maximum runs on the bits of |x| as unsigned:
+// equal to fmaxf's for finite blocks; a NaN then wins (fmaxf would skip it),
+// and such a block is non-finite either way (its sum is NaN), so it stores
+// max + sum as its scale as vx_split_store_b1 does. Levels, c, sum(x) and
+// -8 O are those of vx_split_store_b1 bit for bit.
+template <int N>
+__device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0, uint32_t stride, uint32_t total,
+                                                  const f32x4 (&xv)[N]) {
+    float m[N], inv1[N], inv2[N], s1[N], c[N], sx[N], oz[N];
+    int q1[N][4], q2[N][4];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const f32x4 v = xv[i];
+        const uint32_t mb = max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
+                                max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w))));
+        m[i] = __uint_as_float(vx_umax8(mb));
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        c[i] = m[i] * (1.0f / (127.0f * 254.0f));
+        inv1[i] = m[i] > 0.f ? 127.0f / m[i] : 0.f;
+        inv2[i] = inv1[i] * 254.0f;
+        s1[i] = 254.0f * c[i];
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            q1[i][e] = (int)rintf(xv[i][e] * inv1[i]);
+            const float r = __builtin_fmaf(-(float)q1[i][e], s1[i], xv[i][e]);
+            q2[i][e] = min(127, max(-127, (int)rintf(r * inv2[i])));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        sx[i] = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+        oz[i] = (float)(254 * (q1[i][0] + q1[i][1] + q1[i][2] + q1[i][3]) + (q2[i][0] + q2[i][1] + q2[i][2] + q2[i][3]));
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        sx[i] = vx_sum8(sx[i]);
+        oz[i] = vx_sum8(oz[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const uint32_t f = f0 + stride * (uint32_t)i;
+        if (f < total) {
+            const bool fin = m[i] < __builtin_inff() && sx[i] == sx[i];
+            const uint32_t ul = f >> 4, j = f & 15u;
+            uint32_t* x8 = (uint32_t*)L.x8(0);
+            x8[((0u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[i][0], q1[i][1], q1[i][2], q1[i][3]);
+            x8[((1u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[i][0], q2[i][1], q2[i][2], q2[i][3]);
+            if ((j & 7u) == 0u) {
+                const uint32_t idx = 2u * ul + (j >> 3);
+                L.cs(1, 0)[idx] = fin ? c[i] : m[i] + sx[i];
+                L.sx(1, 0)[idx] = sx[i];
+                L.oz(1, 0)[idx] = -8 * (int)oz[i];
+            }
+        }
+    }
+}
+
 // Batch 1, persistent, on the integer-dot path: the work split, issue order
 // and ring of vx_gemv_p1, with x staged in LDS as two int8 levels per
 // 32-block (the vx_i8lds layout; x ~= c (254 x1 + x2), error <= c / 2 ~
@@ -588,15 +662,21 @@ __device__ __forceinline__ void vx_split_store_b1(const vx_i8lds& L, uint32_t f,
 // (v_cvt_pk_f32_fp8 costs about three times a v_fma_f32), so a unit takes
 // about half the VALU time of vx_unit_dot_b1. Each 8 consecutive lanes
 // stage one 32-block; its max and sums are reduced with DPP.
-template <int QT, int P, int WGT, bool XV>
+template <int QT, int P, int WGT, bool XV, bool XM = false, bool FS = false>
 __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t XW = WGT < 512 ? WGT : 512u;
     constexpr int XPT = (int)(VX_P_XF / XW);
+    static_assert(!FS || XPT % 2 == 0, "the paired split takes whole pairs of rounds");
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t nwv = gridDim.x * (WGT / 64u);
-    const uint32_t gw = wave * gridDim.x + blockIdx.x;  // wave-major, as vx_gemv_p1
+    const uint32_t G = gridDim.x, nwv = G * (WGT / 64u);
+    // XM: workgroups are dealt to the 8 XCDs in turn (workgroup b runs on
+    // XCD b % 8), so position pb = (b % 8) G / 8 + b / 8 gives each XCD a
+    // contiguous range of positions; with wave-major rows (below) each XCD
+    // then streams runs of G / 8 adjacent rows. Identity when G % 8 != 0.
+    const uint32_t pb = (XM && (G & 7u) == 0u) ? (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const uint32_t gw = wave * G + pb;  // wave-major, as vx_gemv_p1
     const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
     const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
     const uint32_t nitems = nrows * npass;
@@ -612,7 +692,9 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     f32x4 xr[XPT];
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-        if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;  // uniform: rounds past x
+        // uniform: rounds past x (FS: whole pairs of rounds, the second
+        // one's lanes past x re-reading the last float4)
+        if ((uint32_t)(FS ? i & ~1 : i) * XW >= total || wave >= XW / 64u) break;
         const uint32_t f = min(t + XW * (uint32_t)i, total - 1u);
         if constexpr (XV) {
             xr[i] = *(const f32x4*)(a.x + 4 * (int64_t)f);
@@ -643,13 +725,23 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         vx_load_unit<QT, true>(rp, u, wr[j]);
     }
 
-    // 3. split x into the two levels and store them (vx_split_store_b1).
+    // 3. split x into the two levels and store them (vx_split_store_b1;
+    //    FS: two rounds at a time, interleaved, vx_split_store_bn).
+    if constexpr (FS) {
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-        if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
-        const uint32_t f = t + XW * (uint32_t)i;
-        const bool in = f < total;
-        vx_split_store_b1(L, f, in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f}, in);
+        for (int i = 0; i < XPT; i += 2) {
+            if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
+            const f32x4 pr[2] = {xr[i], xr[i + 1]};
+            vx_split_store_bn<2>(L, t + XW * (uint32_t)i, XW, total, pr);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) {
+            if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
+            const uint32_t f = t + XW * (uint32_t)i;
+            const bool in = f < total;
+            vx_split_store_b1(L, f, in ? xr[i] : f32x4{0.f, 0.f, 0.f, 0.f}, in);
+        }
     }
     __syncthreads();
 
@@ -703,20 +795,23 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
 }
 
 // Read probe (measurement only): the loads of vx_gemv_p1i with nothing
-// else. Same grid, wave-major row numbering and per-lane units; no x, no
-// barrier, no arithmetic; every item of a round of P in flight before any is
-// used (an empty asm statement consumes each loaded word, so the loads stay
-// and their waits are real), nothing loaded past the wave's last item.
-// Lane 0 writes its XOR of the row's words to y: the bytes of the GEMV
-// without x. Its time is the ceiling of what the GEMV's access pattern can
-// stream in one launch.
+// else. Same grid, per-XCD wave-major row numbering and per-lane units; no
+// x, no barrier, no arithmetic; every item of a round of P in flight before
+// any is used (an empty asm statement consumes each loaded word, so the
+// loads stay and their waits are real), nothing loaded past the wave's last
+// item. Lane 0 writes its XOR of the row's words to y: the bytes of the
+// GEMV without x. Its time is the ceiling of what the GEMV's access pattern
+// can stream in one launch. P = 1, the GEMV's ring for one-pass rows, is
+// also the fastest depth for the bare loads (Q4_0 11008 x 4096: 6.03 us
+// against 6.13 with two items and 6.34 with four).
 template <int QT, int P>
 __device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t nwv = gridDim.x * 16u;
-    const uint32_t gw = wave * gridDim.x + blockIdx.x;
+    const uint32_t G = gridDim.x, nwv = G * 16u;
+    const uint32_t pb = (G & 7u) == 0u ? (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const uint32_t gw = wave * G + pb;
     const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
     const uint32_t nrows = a.M > gw ? (a.M - gw + nwv - 1u) / nwv : 0u;
     const uint32_t nitems = nrows * npass;
@@ -899,13 +994,22 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
         if (a.x_vec) vx_gemv_bn<QT, NB, R, LPR, true>(a);                                         \
         else vx_gemv_bn<QT, NB, R, LPR, false>(a);                                                \
     }
+// Persistent batch-1 kernels: rows per XCD in contiguous runs (XM), and
+// for the integer-dot path the paired split (FS). Same-box A/B, graph-
+// replayed (Q4_0 11008x4096 / Q8_0 4096^2 / Q4_0 4096x11008 / Q4_K
+// 14336x4096 / Q4_K 32000x4096, us): int8 x, ring 2 without either 6.96 /
+// 5.33 / 8.04 / 8.22 / 15.23, ring 1 with both 6.46 / 5.31 / 8.18 / 7.66 /
+// 14.69, ring 2 with both 6.90 / 5.50 / 7.82 / 8.27 / 14.99; f32 x, ring 2
+// 7.72 / 6.61 / 8.71 / 9.92 / 18.49, ring 1 with XM 6.57 / 5.47 / 7.96 /
+// 8.34 / 15.85. Outputs identical bit for bit across all of them.
 #define VX_GEMV_P1(QT, QN, P, WGT)                                                              \
     extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(vx_gemv_args a) {  \
-        if (a.x_vec) vx_gemv_p1<QT, P, WGT, true>(a); else vx_gemv_p1<QT, P, WGT, false>(a);   \
+        if (a.x_vec) vx_gemv_p1<QT, P, WGT, true, true>(a); else vx_gemv_p1<QT, P, WGT, false, true>(a); \
     }
 #define VX_GEMV_P1I(QT, QN, P)                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(vx_gemv_args a) {  \
-        if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true>(a); else vx_gemv_p1i<QT, P, 1024, false>(a); \
+        if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true, true, true>(a);                              \
+        else vx_gemv_p1i<QT, P, 1024, false, true, true>(a);                                     \
     }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
@@ -928,17 +1032,25 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
 VX_GEMV_ALL(VX_Q4_0, q4_0)
 VX_GEMV_ALL(VX_Q8_0, q8_0)
 VX_GEMV_ALL(VX_Q4_K, q4_k)
-VX_GEMV_P1(VX_Q4_0, q4_0, 2, 1024)
+VX_GEMV_P1(VX_Q4_0, q4_0, 1, 1024)
 VX_GEMV_P1(VX_Q8_0, q8_0, 1, 1024)
-VX_GEMV_P1(VX_Q4_K, q4_k, 2, 1024)
+VX_GEMV_P1(VX_Q4_K, q4_k, 1, 1024)
+VX_GEMV_P1I(VX_Q4_0, q4_0, 1)
 VX_GEMV_P1I(VX_Q4_0, q4_0, 2)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
+VX_GEMV_P1I(VX_Q4_K, q4_k, 1)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
 #define VX_READ_PROBE(QT, QN)                                                                     \
     extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(vx_gemv_args a) {      \
-        vx_read_probe<QT, 4>(a);                                                                  \
+        vx_read_probe<QT, 1>(a);                                                                  \
     }
+// Launch floor (measurement only): no work, the batch-1 GEMV's grid. In a
+// replayed HIP graph its time per launch is the fixed cost every kernel of
+// a step pays (dispatch, wave launch, completion) before any byte moves.
+extern "C" __global__ __launch_bounds__(1024) void vx_launch_floor_k(vx_gemv_args a) {
+    if (a.M == 0xFFFFFFFFu && threadIdx.x == 0) a.y[blockIdx.x] = 0.f;  // never true: keeps the argument
+}
 VX_READ_PROBE(VX_Q4_0, q4_0)
 VX_READ_PROBE(VX_Q8_0, q8_0)
 VX_READ_PROBE(VX_Q4_K, q4_k)

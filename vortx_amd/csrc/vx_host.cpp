@@ -492,9 +492,9 @@ static int p1_kernel(uint32_t qt) {
 // Persistent batch-1 kernel on the integer-dot path, by ring depth P (1 or 2).
 static int p1i_kernel(uint32_t qt, int P) {
     switch (q_index(qt)) {
-    case 0: return K_vx_gemv_p1i_q4_0_p2;
+    case 0: return P >= 2 ? K_vx_gemv_p1i_q4_0_p2 : K_vx_gemv_p1i_q4_0_p1;
     case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
-    default: return K_vx_gemv_p1i_q4_k_p2;
+    default: return P >= 2 ? K_vx_gemv_p1i_q4_k_p2 : K_vx_gemv_p1i_q4_k_p1;
     }
 }
 
@@ -887,13 +887,18 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
             lds = (size_t)a.upitch * 152u;
-            // Ring of two items per wave; Q8_0 (68-byte units) with at most two
-            // items per wave takes a ring of one: the second slot would only
-            // load a repeat of the last item (2048 x 4096 4.57 -> 4.09 us,
-            // 4096 x 8192 8.75 -> 8.45 us, 4096 x 4096 5.45 -> 5.42 us).
+            // Ring of one item per wave where a row is one pass (K <= 4096):
+            // fewer requests in flight per wave, and the x loads queue behind
+            // fewer weight requests (Q4_0 11008 x 4096 6.90 -> 6.46 us, Q4_K
+            // 14336 x 4096 8.27 -> 7.66 us). Several passes keep a ring of two
+            // (Q4_0 4096 x 11008 7.82 against 8.18 us with one), except Q8_0
+            // (68-byte units) with at most two items per wave, where the
+            // second slot would only load a repeat of the last item (2048 x
+            // 4096 4.57 -> 4.09 us, 4096 x 8192 8.75 -> 8.45 us).
             const uint32_t waves = (uint32_t)ctx->num_cus * 16u;
-            const uint32_t items = (M + waves - 1u) / waves * ((a.nunits + 63u) / 64u);
-            const int ring = (w->qtype == VX_Q8_0 && items <= 2u) ? 1 : 2;
+            const uint32_t npass = (a.nunits + 63u) / 64u;
+            const uint32_t items = (M + waves - 1u) / waves * npass;
+            const int ring = (npass == 1u || (w->qtype == VX_Q8_0 && items <= 2u)) ? 1 : 2;
             s = launch(ctx, p1i_kernel(w->qtype, ring), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
             if (s) return s;
             b0 += NB;
@@ -976,6 +981,15 @@ static int run_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w, flo
     const int k = q_index(w->qtype) == 0 ? K_vx_read_probe_q4_0 : q_index(w->qtype) == 1 ? K_vx_read_probe_q8_0
                                                                                          : K_vx_read_probe_q4_k;
     return launch(ctx, k, dim3((uint32_t)ctx->num_cus), dim3(1024u), 0, stream, a);
+}
+
+// Launch floor: an empty kernel on the batch-1 GEMV's grid (measurement).
+static int run_launch_floor(vx_ctx ctx, vx_stream stream) {
+    clear_error();
+    if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
+    DeviceGuard guard(ctx->device);
+    vx_gemv_args a{};
+    return launch(ctx, K_vx_launch_floor_k, dim3((uint32_t)ctx->num_cus), dim3(1024u), 0, stream, a);
 }
 
 // ------------------------------------------------------------ contiguous
@@ -1241,6 +1255,8 @@ int vx_gemv_q_xq(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_qweig
 int vx_gemv_q_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w, float* y) {
     return vx::run_read_probe(ctx, stream, w, y);
 }
+
+int vx_launch_floor(vx_ctx ctx, vx_stream stream) { return vx::run_launch_floor(ctx, stream); }
 
 int vx_dequantize(vx_ctx ctx, vx_stream stream, const vx_mview* out, const vx_qweight* w) {
     return vx::run_dequant(ctx, stream, out, w);
