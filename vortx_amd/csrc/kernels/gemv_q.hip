@@ -1256,7 +1256,7 @@ __device__ __align__(256) uint8_t vx_scratch[VX_SCRATCH_BYTES];
 // Per wave, after the scales: the fused split's tables ([64] {m, S}, then
 // [64] {c1, i1, i2, fin}), 1536 bytes.
 #define VX_XQ_FX_FLOAT2 192u
-template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX, bool FH>
+template <int QT, int NCG, int XI, int RD, bool MP, bool ST, bool FX, bool FH, bool XM = false>
 __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t CP = 8u * NCG;             // columns per launch (padded)
@@ -1268,7 +1268,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t n = lane & 15u, g = lane >> 4;
-    const uint32_t G = gridDim.x, cu = blockIdx.x;
+    const uint32_t G = gridDim.x;
+    // XM: positions per XCD as in vx_gemv_p1i (workgroup b runs on XCD b % 8)
+    const uint32_t cu = (XM && (G & 7u) == 0u) ? (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     // this CU's tile-work ts covers rows rb + ts rs .. + 15, below rlim:
     // rows [r0, r1), M split into G ranges that differ by at most one row,
     // in 16-row tiles (the last one possibly partial), or with two column
@@ -1663,12 +1665,17 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
         if (nfull + (uint32_t)u < nwork) tile_work(nfull + (uint32_t)u, u, true);
 }
 
+// One column group: CU positions per XCD (XM; same-box A/B, graph-replayed:
+// Q4_0 11008x4096 B = 8 fused 10.25 -> 9.97 us, 4096x11008 B = 8 on a split
+// 9.51 -> 9.43, Q8_0 4096^2 B = 8 7.51 -> 7.44). Two column groups keep the
+// plain order (Q4_K 32000x4096 B = 16 27.96 against 28.41 us with XM).
 #define VX_GEMV_XQ(QT, QN, NCG, XI, RD, MP, ST, FX, SFX, FH)                                       \
     extern "C" __global__ __launch_bounds__(VX_XQ_WG) void vx_gemv_xq_##QN##_c##NCG##_x##XI##SFX(vx_gemv_xq_args a) { \
-        vx_gemv_xq<QT, NCG, XI, RD, MP, ST, FX, FH>(a);                                                 \
+        vx_gemv_xq<QT, NCG, XI, RD, MP, ST, FX, FH, NCG == 1>(a);                                        \
     }
 // (column groups NCG, items per wave and pass XI, ring depth RD in tiles):
-// RD * XI weight items in flight per wave, as many as the registers allow.
+// RD * XI weight items in flight per wave, as many as the registers allow
+// except Q4_0 with one item (measured best at 3 of the 4 that fit).
 // One pass (K <= 4096 XI): exact waits; _mp: several passes; _st: one pass
 // with at most RD tile-works per wave (no loop); _fx: x split in the kernel
 // (x f32 with stride 1 along K) instead of read from a vx_quantize_x split.
@@ -1688,7 +1695,9 @@ __device__ __forceinline__ void vx_gemv_xq(const vx_gemv_xq_args& a) {
     VX_GEMV_XQ1(QT, QN, 1, 1, RD)                              \
     VX_GEMV_XQF(QT, QN, 1, 1, RD)                              \
     VX_GEMV_XQF4(QT, QN, 1, RD)
-VX_GEMV_XQ1F(VX_Q4_0, q4_0, 4)
+// Q4_0, one item per wave: a ring of 3 tile-works (4: 9.97 -> 9.77 us at
+// 11008x4096 B = 8, 9.12 -> 8.89 at B = 4; 2: 10.29 us)
+VX_GEMV_XQ1F(VX_Q4_0, q4_0, 3)
 VX_GEMV_XQ1(VX_Q4_0, q4_0, 1, 2, 1)
 VX_GEMV_XQF(VX_Q4_0, q4_0, 1, 2, 1)
 VX_GEMV_XQF4(VX_Q4_0, q4_0, 2, 1)

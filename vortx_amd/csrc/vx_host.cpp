@@ -589,7 +589,7 @@ static int run_quantize_x(vx_ctx ctx, vx_stream stream, const vx_xq* q, const vx
 // instantiated in gemv_q.hip.
 static int xq_ring(uint32_t qt, int ncg, int xi) {
     switch (q_index(qt)) {
-    case 0: return ncg == 2 ? 3 : xi == 1 ? 4 : 1;
+    case 0: return ncg == 2 ? 3 : xi == 1 ? 3 : 1;
     case 1: return ncg == 2 ? 2 : xi == 1 ? 2 : 1;
     default: return ncg == 2 ? 2 : xi == 1 ? 3 : 1;
     }
