@@ -591,61 +591,62 @@ __device__ __forceinline__ uint32_t vx_umax8(uint32_t v) {
 
 // vx_split_store_b1 for N float4 per lane (f, f + stride, ...), the N
 // dependency chains interleaved step by step so their DPP reductions and
-// divisions overlap. The block maximum runs on the bits of |x| as unsigned:
-// equal to fmaxf's for finite blocks; a NaN then wins (fmaxf would skip it),
-// and such a block is non-finite either way (its sum is NaN), so it stores
-// max + sum as its scale as vx_split_store_b1 does. Levels, c, sum(x) and
-// -8 O are those of vx_split_store_b1 bit for bit.
+// divisions overlap, and each level computed with one rounding
+// (vx_xq_levels4: q1 = RNE(v inv1) and q2 = RNE(r inv2) from fmaf(., ., 1.5
+// 2^23), the bytes gathered with v_perm_b32; 4 VALU per element instead of
+// 9). The block maximum runs on the bits of |x| as unsigned: equal to
+// fmaxf's for finite blocks; a NaN then wins (fmaxf would skip it), and such
+// a block is non-finite either way (its sum is NaN). Scales as in
+// vx_split_store_b1 (c = m / (127 254), inv1 = 127 / m); the clamps to +-127
+// never act: |v inv1| <= 127 (1 + 2^-24), and with r = RN(v - q1 s1),
+// |r inv2| <= 254 (0.5 + 508 2^-24)(1 + 3 2^-24) < 127.01. A block with m <
+// 2^-100 (inv1 would overflow) or non-finite stores zero levels; a
+// non-finite one stores max + sum as its scale, so y is non-finite. O =
+// sum(254 q1 + q2) comes from the packed bytes (v_dot4 against 0x01010101).
 template <int N>
 __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0, uint32_t stride, uint32_t total,
                                                   const f32x4 (&xv)[N]) {
-    float m[N], inv1[N], inv2[N], s1[N], c[N], sx[N], oz[N];
-    int q1[N][4], q2[N][4];
+    float m[N], c[N], inv1[N], inv2[N], s1[N], sx[N], oz[N];
+    bool fin[N];
+    uint32_t w1[N], w2[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const f32x4 v = xv[i];
         const uint32_t mb = max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
                                 max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w))));
         m[i] = __uint_as_float(vx_umax8(mb));
+        sx[i] = (v.x + v.y) + (v.z + v.w);
     }
 #pragma unroll
+    for (int i = 0; i < N; ++i) sx[i] = vx_sum8(sx[i]);
+#pragma unroll
     for (int i = 0; i < N; ++i) {
+        fin[i] = m[i] < __builtin_inff() && sx[i] == sx[i];
         c[i] = m[i] * (1.0f / (127.0f * 254.0f));
-        inv1[i] = m[i] > 0.f ? 127.0f / m[i] : 0.f;
+        inv1[i] = (fin[i] && m[i] >= 0x1p-100f) ? 127.0f / m[i] : 0.f;
         inv2[i] = inv1[i] * 254.0f;
         s1[i] = 254.0f * c[i];
     }
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            q1[i][e] = (int)rintf(xv[i][e] * inv1[i]);
-            const float r = __builtin_fmaf(-(float)q1[i][e], s1[i], xv[i][e]);
-            q2[i][e] = min(127, max(-127, (int)rintf(r * inv2[i])));
-        }
+        vx_xq_levels4(xv[i], s1[i], inv1[i], inv2[i], fin[i], w1[i], w2[i]);
+        const int o = 254 * __builtin_amdgcn_sdot4((int)w1[i], 0x01010101, 0, false) +
+                      __builtin_amdgcn_sdot4((int)w2[i], 0x01010101, 0, false);
+        oz[i] = (float)o;
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-        sx[i] = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
-        oz[i] = (float)(254 * (q1[i][0] + q1[i][1] + q1[i][2] + q1[i][3]) + (q2[i][0] + q2[i][1] + q2[i][2] + q2[i][3]));
-    }
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        sx[i] = vx_sum8(sx[i]);
-        oz[i] = vx_sum8(oz[i]);
-    }
+    for (int i = 0; i < N; ++i) oz[i] = vx_sum8(oz[i]);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const uint32_t f = f0 + stride * (uint32_t)i;
         if (f < total) {
-            const bool fin = m[i] < __builtin_inff() && sx[i] == sx[i];
             const uint32_t ul = f >> 4, j = f & 15u;
             uint32_t* x8 = (uint32_t*)L.x8(0);
-            x8[((0u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q1[i][0], q1[i][1], q1[i][2], q1[i][3]);
-            x8[((1u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = vx_pack4(q2[i][0], q2[i][1], q2[i][2], q2[i][3]);
+            x8[((0u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = w1[i];
+            x8[((1u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = w2[i];
             if ((j & 7u) == 0u) {
                 const uint32_t idx = 2u * ul + (j >> 3);
-                L.cs(1, 0)[idx] = fin ? c[i] : m[i] + sx[i];
+                L.cs(1, 0)[idx] = fin[i] ? c[i] : m[i] + sx[i];
                 L.sx(1, 0)[idx] = sx[i];
                 L.oz(1, 0)[idx] = -8 * (int)oz[i];
             }
