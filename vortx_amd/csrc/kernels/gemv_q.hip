@@ -663,7 +663,11 @@ __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0
 // (v_cvt_pk_f32_fp8 costs about three times a v_fma_f32), so a unit takes
 // about half the VALU time of vx_unit_dot_b1. Each 8 consecutive lanes
 // stage one 32-block; its max and sums are reduced with DPP.
-template <int QT, int P, int WGT, bool XV, bool XM = false, bool FS = false>
+// EW (one item per wave): no bare barrier after the x loads, so every wave
+// requests its one item as soon as it starts (Q8_0 4096^2 5.37 -> 5.15 us);
+// with more items per wave the x must come first (Q4_0 11008 x 4096 6.38
+// against 6.54 us without the barrier).
+template <int QT, int P, int WGT, bool XV, bool XM = false, bool FS = false, bool EW = false>
 __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t XW = WGT < 512 ? WGT : 512u;
@@ -705,7 +709,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         }
     }
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
+    if constexpr (!EW) __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
     // 2. the first ring items (see vx_gemv_p1 for the clamping).
@@ -1012,6 +1016,12 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
         if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true, true, true>(a);                              \
         else vx_gemv_p1i<QT, P, 1024, false, true, true>(a);                                     \
     }
+// _p1e: one item per wave (every row one pass, at most one row per wave)
+#define VX_GEMV_P1IE(QT, QN)                                                                    \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p1e(vx_gemv_args a) {   \
+        if (a.x_vec) vx_gemv_p1i<QT, 1, 1024, true, true, true, true>(a);                        \
+        else vx_gemv_p1i<QT, 1, 1024, false, true, true, true>(a);                               \
+    }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
     VX_GEMV_B1(QT, QN, 2)                                                                           \
@@ -1042,6 +1052,9 @@ VX_GEMV_P1I(VX_Q8_0, q8_0, 1)
 VX_GEMV_P1I(VX_Q8_0, q8_0, 2)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 1)
 VX_GEMV_P1I(VX_Q4_K, q4_k, 2)
+VX_GEMV_P1IE(VX_Q4_0, q4_0)
+VX_GEMV_P1IE(VX_Q8_0, q8_0)
+VX_GEMV_P1IE(VX_Q4_K, q4_k)
 #define VX_READ_PROBE(QT, QN)                                                                     \
     extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(vx_gemv_args a) {      \
         vx_read_probe<QT, 1>(a);                                                                  \

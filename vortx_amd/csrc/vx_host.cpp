@@ -489,8 +489,12 @@ static int p1_kernel(uint32_t qt) {
     return tab[q_index(qt)];
 }
 
-// Persistent batch-1 kernel on the integer-dot path, by ring depth P (1 or 2).
+// Persistent batch-1 kernel on the integer-dot path, by ring depth P (1 or
+// 2); P = 0: the one-item-per-wave form (_p1e).
 static int p1i_kernel(uint32_t qt, int P) {
+    if (P == 0)
+        return q_index(qt) == 0 ? K_vx_gemv_p1i_q4_0_p1e : q_index(qt) == 1 ? K_vx_gemv_p1i_q8_0_p1e
+                                                                             : K_vx_gemv_p1i_q4_k_p1e;
     switch (q_index(qt)) {
     case 0: return P >= 2 ? K_vx_gemv_p1i_q4_0_p2 : K_vx_gemv_p1i_q4_0_p1;
     case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
@@ -898,7 +902,9 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             const uint32_t waves = (uint32_t)ctx->num_cus * 16u;
             const uint32_t npass = (a.nunits + 63u) / 64u;
             const uint32_t items = (M + waves - 1u) / waves * npass;
-            const int ring = (npass == 1u || (w->qtype == VX_Q8_0 && items <= 2u)) ? 1 : 2;
+            // One item per wave: no barrier between the x and the weight
+            // requests (_p1e; Q8_0 4096 x 4096 5.37 -> 5.15 us).
+            const int ring = items == 1u ? 0 : (npass == 1u || (w->qtype == VX_Q8_0 && items <= 2u)) ? 1 : 2;
             s = launch(ctx, p1i_kernel(w->qtype, ring), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
             if (s) return s;
             b0 += NB;
