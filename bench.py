@@ -19,12 +19,15 @@ GEMM shapes and the broadcast batch; then the GGUF upload, the reference's
 GEMM size sweep (examples/gemm_bench.rs: 64..4096, tiled and naive) and
 CPU baselines from the oracle's OpenMP restatements on the host cores.
 
-Timing: `value` is whole-job throughput: K steps replayed from a HIP graph
-(captured eager launches) between two synchronizations (wall clock).
-`roofline.achieved` divides the algorithmic bytes (or flops) of one step by
-the step's average duration from HIP events recorded on the stream the
-kernels run on, bracketing the same timed region (a two-launch batched step
-counts both launches; its GEMV kernel alone is reported as `gemv_only`).
+Timing: exactly K steps replayed from HIP graphs of captured launches
+between two synchronizations; the timed region is bracketed by HIP events
+recorded on the stream the kernels run on, and `ms_per_step` / `value` /
+`roofline.achieved` are that region's duration per step and the algorithmic
+bytes (or flops) over it (a two-launch batched step counts both launches;
+its GEMV kernel alone is reported as `gemv_only`). `wall_ms_per_step` is
+the wall clock between the two synchronizations per step (host-side graph
+launch and synchronization included). A graph replay carries ~8-10 us of its
+own, so short runs (--steps 20) read ~0.4 us per step above long ones.
 rocprofv3 summaries of the same command are kept under profiles/. Nothing
 goes to stderr without --verbose.
 
@@ -85,35 +88,52 @@ def load_traffic(name: str):
     return None
 
 
+def per_step(done: int, wall: float, ev_ms: float, work: float, scale: float = 1e9) -> dict:
+    """ms_per_step and value (work per step / scale per second) from the
+    event-timed region, and the wall clock per step beside them."""
+    ms = ev_ms / done
+    return {"steps": done, "ms_per_step": ms, "step_ms_events": ms, "value": work / (ms * 1e-3) / scale,
+            "wall_ms_per_step": wall * 1e3 / done}
+
+
 def graph_time(launch, steps: int):
-    """Capture min(steps, 500) launches (launch(i, stream)) into a HIP graph
-    on a side stream and replay it steps // that many times between two
-    synchronizations. Returns (launches done, wall seconds, HIP-event ms on
-    the stream the kernels run on)."""
+    """Exactly `steps` launches (launch(i, stream)) on a side stream, captured
+    min(steps, 500) at a time into a HIP graph (the remainder into a second
+    one) and replayed between two synchronizations after one untimed replay;
+    HIP events on that stream bracket exactly the timed launches. Each replay
+    carries ~8-10 us of its own on the GPU (at 20 steps of a 6.4 us kernel,
+    0.4-0.5 us per step; at 500, 0.02). Returns (launches done, wall seconds
+    between the synchronizations, HIP-event ms of the timed launches)."""
     import torch
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    chunk = min(steps, 500)
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(chunk):
-                launch(i, s)
-    torch.cuda.synchronize()
-    reps = max(1, steps // chunk)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    chunk = min(steps, 500)
+    reps, rem = divmod(steps, chunk)
+    graphs = []
+    for n in (chunk, rem):
+        if n:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    for i in range(n):
+                        launch(i, s)
+            graphs.append(g)
+    torch.cuda.synchronize()
     with torch.cuda.stream(s):  # replay() launches on the current stream
-        graph.replay()
+        graphs[0].replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         e0.record(s)
         for _ in range(reps):
-            graph.replay()
+            graphs[0].replay()
+        if rem:
+            graphs[1].replay()
         e1.record(s)
         torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return reps * chunk, wall, e0.elapsed_time(e1)
+    return steps, wall, e0.elapsed_time(e1)
 
 
 def weight_copies(qtype: int, M: int, K: int, dev):
@@ -160,8 +180,7 @@ def time_gemv(qtype: int, M: int, K: int, B: int, steps: int, warmup: int, label
     torch.cuda.synchronize()
     done, wall, ev_ms = graph_time(fn, steps)
     alg = M * S.row_bytes(qtype, K) + 4 * M if probe else gemv_bytes(qtype, M, K, B)
-    r = {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
-         "step_ms_events": ev_ms / done, "alg_bytes": alg, "weight_copies": ncopy, "launches_per_step": 1}
+    r = dict(per_step(done, wall, ev_ms, alg), alg_bytes=alg, weight_copies=ncopy, launches_per_step=1)
     # the library's route with a workspace (xq_fused_ok in vx_host.cpp): the
     # GEMV splits x itself (one launch) with one pass and one 256-weight item
     # per wave (B <= 16), two with B <= 8 or three with B <= 4, except two
@@ -196,7 +215,7 @@ def time_launch_floor(steps: int, warmup: int):
         g.launch_floor()
     torch.cuda.synchronize()
     done, wall, ev = graph_time(lambda i, s: g.launch_floor(stream=s), steps)
-    return {"steps": done, "ms_per_step": wall * 1e3 / done, "step_ms_events": ev / done}
+    return dict(per_step(done, wall, ev, 0.0))
 
 
 def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
@@ -222,8 +241,7 @@ def time_gemv_f32(M: int, K: int, steps: int, warmup: int):
     torch.cuda.synchronize()
     done, wall, ev = graph_time(lambda i, s: gm.dispatch(y, As[i % ncopy], x, stream=s), steps)
     alg = 4 * M * K + 4 * K + 4 * M
-    return {"steps": done, "ms_per_step": wall * 1e3 / done, "value": alg * done / wall / 1e9,
-            "step_ms_events": ev / done, "alg_bytes": alg, "copies": ncopy}
+    return dict(per_step(done, wall, ev, alg), alg_bytes=alg, copies=ncopy)
 
 
 def event_time(fn, steps: int, warmup: int):
@@ -285,8 +303,7 @@ def time_gemm(M: int, N: int, K: int, steps: int, warmup: int, transb: bool = Fa
     gm = vx.Gemm(0)
     wall, ev = event_time(lambda: gm.dispatch(c, a, b), steps, warmup)
     flops = 2.0 * M * N * K
-    return {"value": flops * steps / wall / 1e12, "step_ms_events": ev / steps, "flops": flops,
-            "ms_per_step": wall * 1e3 / steps, "steps": steps}
+    return dict(per_step(steps, wall, ev, flops, 1e12), flops=flops)
 
 
 def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int):
@@ -305,8 +322,7 @@ def time_gemm_broadcast(B: int, M: int, N: int, K: int, steps: int, warmup: int)
     gm = vx.Gemm(0)
     wall, ev = event_time(lambda: gm.dispatch_ex(c, a, w, alpha=1.0, beta=1.0, broadcast=True), steps, warmup)
     flops = 2.0 * B * M * N * K
-    return {"value": flops * steps / wall / 1e12, "step_ms_events": ev / steps, "flops": flops,
-            "ms_per_step": wall * 1e3 / steps, "steps": steps}
+    return dict(per_step(steps, wall, ev, flops, 1e12), flops=flops)
 
 
 def time_copy_like_gemv(nelem: int, steps: int, warmup: int):
@@ -330,8 +346,7 @@ def time_copy_like_gemv(nelem: int, steps: int, warmup: int):
     torch.cuda.synchronize()
     done, wall, ev = graph_time(lambda i, s: c.launch(out, srcs[i % nsrc], stream=s), steps)
     nbytes = 8 * out.numel()
-    return {"value": nbytes * done / wall / 1e9, "step_ms_events": ev / done,
-            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / done, "sources": nsrc}
+    return dict(per_step(done, wall, ev, nbytes), alg_bytes=nbytes, sources=nsrc)
 
 
 def time_contiguous(shape, steps: int, warmup: int, transposed: bool = True):
@@ -352,8 +367,7 @@ def time_contiguous(shape, steps: int, warmup: int, transposed: bool = True):
     it = iter(range(1 << 30))
     wall, ev = event_time(lambda: c.launch(out, srcs[next(it) % 4]), steps, warmup)
     nbytes = 8 * out.numel()
-    return {"value": nbytes * steps / wall / 1e9, "step_ms_events": ev / steps,
-            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
+    return dict(per_step(steps, wall, ev, nbytes), alg_bytes=nbytes)
 
 
 def time_quantize(qtype: int, M: int, K: int, steps: int, warmup: int):
@@ -373,8 +387,7 @@ def time_quantize(qtype: int, M: int, K: int, steps: int, warmup: int):
     it = iter(range(1 << 30))
     wall, ev = event_time(lambda: qg.quantize(w, xs[next(it) % 2]), steps, warmup)
     nbytes = 4 * M * K + buf.numel()
-    return {"value": nbytes * steps / wall / 1e9, "step_ms_events": ev / steps,
-            "alg_bytes": nbytes, "ms_per_step": wall * 1e3 / steps}
+    return dict(per_step(steps, wall, ev, nbytes), alg_bytes=nbytes)
 
 
 def time_quantize_x(K: int, B: int, steps: int, warmup: int):
@@ -395,8 +408,7 @@ def time_quantize_x(K: int, B: int, steps: int, warmup: int):
     torch.cuda.synchronize()
     done, wall, ev = graph_time(lambda i, s: g.quantize_x(q, x.t(), stream=s), steps)
     nbytes = 4 * B * K + vx.xq_size(K, B)
-    return {"value": nbytes * done / wall / 1e9, "step_ms_events": ev / done, "alg_bytes": nbytes,
-            "ms_per_step": wall * 1e3 / done}
+    return dict(per_step(done, wall, ev, nbytes), alg_bytes=nbytes)
 
 
 def time_gguf_upload(steps: int):
@@ -671,6 +683,7 @@ def main() -> int:
         "steps": q40["steps"],
         "warmup": args.warmup,
         "ms_per_step": rnd(q40["ms_per_step"]),
+        "wall_ms_per_step": rnd(q40["wall_ms_per_step"]),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -678,7 +691,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "Q4_0 GEMV y=Wx, W 11008x4096 (GGML Q4_0 blocks), batch 1",
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
-                   "bytes_per_step": q40["alg_bytes"], "timing": "HIP-graph replay of eager launches",
+                   "bytes_per_step": q40["alg_bytes"],
+                   "timing": "HIP-graph replay of eager launches, HIP events around exactly the timed steps",
                    "x_repr": X_REPR},
         "roofline": roof(q40, "gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
