@@ -28,9 +28,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 #define TBK 16
 #define LDS_PAD 4
-#ifndef VX_ILV
-#define VX_ILV 2  // k-pairs of a stage multiplied before the other buffer's LDS stores
-#endif
 
 // Operand access modes (chosen on the host from strides and alignment).
 #define MODE_KC 0  // contiguous along K, rows 16-byte aligned
@@ -268,29 +265,33 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
             __syncthreads();
             // Invariant at the top: stage st in buffer 0, stage st + 1 in
             // flight to ra1 / rb1.
-            // The other buffer's stores go in after the first VX_ILV k-pairs
-            // of a stage (its last readers finished before the previous
-            // barrier), so the matrix pipes still hold the stage's remaining
-            // MFMAs when the wave reaches the barrier: 4096 x 11008 x 4096
-            // 127.3 -> 131.9 TFLOP/s, 4096^3 (wide) 137.5 -> 139.6 (same-box
-            // A/B; 4 k-pairs 130.3 / 137.3). The bits do not change.
+            // The other buffer's stores go in among the stage's MFMAs (its
+            // last readers finished before the previous barrier): A's after
+            // the first k-pair, B's after the third, so the matrix pipes
+            // still hold the stage's remaining MFMAs when the wave reaches
+            // the barrier. Stores after all eight k-pairs, then after two,
+            // then split 1 / 3 (same-box A/B, TFLOP/s): 4096 x 11008 x 4096
+            // 127.3 -> 131.9 -> 133.0, 4096^3 (wide) 137.5 -> 139.6 -> 141.3,
+            // 2048^3 113.5 -> 118.6 -> 121.7. The bits do not change.
             uint32_t st = 0;
             for (; st + 2u <= nkf; st += 2u) {
                 ld(st + 2u, ra0, rb0);
                 // keep the loads above the MFMAs (the scheduler would sink them
                 // below the other buffer's store and share its registers)
                 __builtin_amdgcn_sched_barrier(0);
-                mma_part(0u, 0, VX_ILV);
+                mma_part(0u, 0, 1);
                 vx_store_frag<AMODE, TM, LDA>(ra1, As[1]);
+                mma_part(0u, 1, 3);
                 vx_store_frag<BMODE, TN, LDB>(rb1, Bs[1]);
-                mma_part(0u, VX_ILV, TBK / 2);
+                mma_part(0u, 3, TBK / 2);
                 __syncthreads();
                 ld(st + 3u, ra1, rb1);
                 __builtin_amdgcn_sched_barrier(0);
-                mma_part(1u, 0, VX_ILV);
+                mma_part(1u, 0, 1);
                 vx_store_frag<AMODE, TM, LDA>(ra0, As[0]);
+                mma_part(1u, 1, 3);
                 vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
-                mma_part(1u, VX_ILV, TBK / 2);
+                mma_part(1u, 3, TBK / 2);
                 __syncthreads();
             }
             if (st < nkf) mma(0u);  // an odd stage count: the last one
