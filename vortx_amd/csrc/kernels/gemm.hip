@@ -273,26 +273,36 @@ __device__ __forceinline__ void vx_gemm_mfma(const vx_gemm_args& p) {
             // then split 1 / 3 (same-box A/B, TFLOP/s): 4096 x 11008 x 4096
             // 127.3 -> 131.9 -> 133.0, 4096^3 (wide) 137.5 -> 139.6 -> 141.3,
             // 2048^3 113.5 -> 118.6 -> 121.7. The bits do not change.
+            // Narrow and small tiles (TN <= 128) issue the next loads after
+            // B's stores, wide tiles at the top of the stage (same-box A/B,
+            // TFLOP/s, loads at the top / after B's stores: 128 x 128 tiles
+            // 4096 x 11008 x 4096 132.9 / 135.2, 4096^3 134.8 / 137.0, 2048^3
+            // 117.6 / 124.0; 128 x 256 tiles 4096^3 140.8 / 140.3).
+            constexpr bool LATE_LD = TN <= 128;
+            auto half = [&](uint32_t buf, vx_frag<AMODE, TM>& sa, vx_frag<BMODE, TN>& sb, vx_frag<AMODE, TM>& la,
+                            vx_frag<BMODE, TN>& lb, uint32_t ns) {
+                if (!LATE_LD) {
+                    ld(ns, la, lb);
+                    // keep the loads above the MFMAs (the scheduler would sink
+                    // them below the other buffer's store and share its registers)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                mma_part(buf, 0, 1);
+                vx_store_frag<AMODE, TM, LDA>(sa, As[buf ^ 1u]);
+                mma_part(buf, 1, 3);
+                vx_store_frag<BMODE, TN, LDB>(sb, Bs[buf ^ 1u]);
+                if (LATE_LD) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    ld(ns, la, lb);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                mma_part(buf, 3, TBK / 2);
+                __syncthreads();
+            };
             uint32_t st = 0;
             for (; st + 2u <= nkf; st += 2u) {
-                ld(st + 2u, ra0, rb0);
-                // keep the loads above the MFMAs (the scheduler would sink them
-                // below the other buffer's store and share its registers)
-                __builtin_amdgcn_sched_barrier(0);
-                mma_part(0u, 0, 1);
-                vx_store_frag<AMODE, TM, LDA>(ra1, As[1]);
-                mma_part(0u, 1, 3);
-                vx_store_frag<BMODE, TN, LDB>(rb1, Bs[1]);
-                mma_part(0u, 3, TBK / 2);
-                __syncthreads();
-                ld(st + 3u, ra1, rb1);
-                __builtin_amdgcn_sched_barrier(0);
-                mma_part(1u, 0, 1);
-                vx_store_frag<AMODE, TM, LDA>(ra0, As[0]);
-                mma_part(1u, 1, 3);
-                vx_store_frag<BMODE, TN, LDB>(rb0, Bs[0]);
-                mma_part(1u, 3, TBK / 2);
-                __syncthreads();
+                half(0u, ra1, rb1, ra0, rb0, st + 2u);
+                half(1u, ra0, rb0, ra1, rb1, st + 3u);
             }
             if (st < nkf) mma(0u);  // an odd stage count: the last one
         }
