@@ -535,8 +535,11 @@ KEYS = (["gemv_q4_0_11008x4096_b1", "gemv_q8_0_4096x4096_b1", "gemv_q4_0_11008x4
          "gemv_f32_32768x4096"] + list(GEMMS) +
         ["gemm_f32_broadcast_8x1024", "gemm_sweep", "contiguous_t8192", "copy_8192", "copy_3104x1024",
          "quantize_q8_0_14336x4096", "quantize_q4_k_14336x4096", "gguf_upload"])
-# GEMMs: at least this many timed launches after this many warmups, whatever --steps is
-GEMM_STEPS, GEMM_WARMUP = 50, 10
+# GEMMs: this many timed launches after this many warmups, whatever --steps is;
+# 50 warmups (~50 ms at 4096^3) because after the idle gap of the workload's
+# set-up the clocks need tens of ms to come back (10 warmups read 4096^3 at
+# 136 TFLOP/s where a warm GPU runs it at 140)
+GEMM_STEPS, GEMM_WARMUP = 50, 50
 
 
 def run_workloads(keys, steps: int, warmup: int) -> dict:
