@@ -166,6 +166,32 @@ def test_gemv_x_edge_values(qgemv, qtype):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("M,K", [(40, 4096), (11008, 4096), (600, 8192)], ids=["one-item", "one-pass", "two-pass"])
+def test_gemv_persistent_x_edge_values(qgemv, qtype, M, K):
+    """The persistent batch-1 kernels (one item per wave, one pass, several
+    passes) with x blocks that are all zero, tiny above and below 2^-100
+    (the latter stored as zero levels), huge, subnormal, or one large outlier
+    among small values, split in the kernel; y within tolerance of the
+    float64 product."""
+    note(f"gemv persistent edge x {QN[qtype]} M={M} K={K}")
+    w = S.quant_weights(qtype, M, K, seed=13, device=DEV)
+    x = S.activations(1, K, seed=14, device=DEV)
+    x[0, 0:32] = 0.0
+    x[0, 32:64] *= 1e-30
+    x[0, 64:96] *= 1e-33
+    x[0, 96:128] *= 1e30
+    x[0, 128:160] *= 1e-3
+    x[0, 140] = 50.0
+    x[0, 160:192] = 1e-40
+    x[0, K - 32:K] *= 1e-20
+    y = torch.full((M,), float("nan"), device=DEV)
+    ref = O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy())[:, 0]
+    qgemv.dispatch(y, vx.QWeight(w, qtype, M, K), x[0])
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy(), ref, what="persistent int8-x")
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 @pytest.mark.parametrize("B", [2, 5, 8, 9])
 def test_gemv_batched_x_edge_values(qgemv, qtype, B):
     """Batched (matrix-core) path: per column, blocks of x that are zero,

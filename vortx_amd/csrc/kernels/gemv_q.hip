@@ -601,11 +601,16 @@ __device__ __forceinline__ uint32_t vx_umax8(uint32_t v) {
 // never act: |v inv1| <= 127 (1 + 2^-24), and with r = RN(v - q1 s1),
 // |r inv2| <= 254 (0.5 + 508 2^-24)(1 + 3 2^-24) < 127.01. A block with m <
 // 2^-100 (inv1 would overflow) or non-finite stores zero levels; a
-// non-finite one stores max + sum as its scale, so y is non-finite. O =
-// sum(254 q1 + q2) comes from the packed bytes (v_dot4 against 0x01010101).
-template <int N>
+// non-finite one stores a non-finite scale, so y is non-finite. Only the
+// block sums the format's decode uses are formed: sum(x) for Q4_K's min
+// term, O = sum(254 q1 + q2) for Q4_0's zero point (from the packed bytes,
+// v_dot4 against 0x01010101), neither for Q8_0. The maximum on the bits
+// sees a NaN (it orders above infinity), so m < inf alone tells a finite
+// block.
+template <int QT, int N>
 __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0, uint32_t stride, uint32_t total,
                                                   const f32x4 (&xv)[N]) {
+    constexpr bool SX = QT == VX_Q4_K, OZ = QT == VX_Q4_0;
     float m[N], c[N], inv1[N], inv2[N], s1[N], sx[N], oz[N];
     bool fin[N];
     uint32_t w1[N], w2[N];
@@ -615,13 +620,15 @@ __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0
         const uint32_t mb = max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
                                 max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w))));
         m[i] = __uint_as_float(vx_umax8(mb));
-        sx[i] = (v.x + v.y) + (v.z + v.w);
+        if (SX) sx[i] = (v.x + v.y) + (v.z + v.w);
+    }
+    if (SX) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) sx[i] = vx_sum8(sx[i]);
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i) sx[i] = vx_sum8(sx[i]);
-#pragma unroll
     for (int i = 0; i < N; ++i) {
-        fin[i] = m[i] < __builtin_inff() && sx[i] == sx[i];
+        fin[i] = m[i] < __builtin_inff();
         c[i] = m[i] * (1.0f / (127.0f * 254.0f));
         inv1[i] = (fin[i] && m[i] >= 0x1p-100f) ? 127.0f / m[i] : 0.f;
         inv2[i] = inv1[i] * 254.0f;
@@ -630,12 +637,16 @@ __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         vx_xq_levels4(xv[i], s1[i], inv1[i], inv2[i], fin[i], w1[i], w2[i]);
-        const int o = 254 * __builtin_amdgcn_sdot4((int)w1[i], 0x01010101, 0, false) +
-                      __builtin_amdgcn_sdot4((int)w2[i], 0x01010101, 0, false);
-        oz[i] = (float)o;
+        if (OZ) {
+            const int o = 254 * __builtin_amdgcn_sdot4((int)w1[i], 0x01010101, 0, false) +
+                          __builtin_amdgcn_sdot4((int)w2[i], 0x01010101, 0, false);
+            oz[i] = (float)o;
+        }
     }
+    if (OZ) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) oz[i] = vx_sum8(oz[i]);
+        for (int i = 0; i < N; ++i) oz[i] = vx_sum8(oz[i]);
+    }
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         const uint32_t f = f0 + stride * (uint32_t)i;
@@ -646,9 +657,9 @@ __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0
             x8[((1u * 4u + (j >> 2)) * L.upitch + ul) * 4u + (j & 3u)] = w2[i];
             if ((j & 7u) == 0u) {
                 const uint32_t idx = 2u * ul + (j >> 3);
-                L.cs(1, 0)[idx] = fin[i] ? c[i] : m[i] + sx[i];
-                L.sx(1, 0)[idx] = sx[i];
-                L.oz(1, 0)[idx] = -8 * (int)oz[i];
+                L.cs(1, 0)[idx] = fin[i] ? c[i] : m[i];
+                if (SX) L.sx(1, 0)[idx] = sx[i];
+                if (OZ) L.oz(1, 0)[idx] = -8 * (int)oz[i];
             }
         }
     }
@@ -737,7 +748,7 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
         for (int i = 0; i < XPT; i += 2) {
             if ((uint32_t)i * XW >= total || wave >= XW / 64u) break;
             const f32x4 pr[2] = {xr[i], xr[i + 1]};
-            vx_split_store_bn<2>(L, t + XW * (uint32_t)i, XW, total, pr);
+            vx_split_store_bn<QT, 2>(L, t + XW * (uint32_t)i, XW, total, pr);
         }
     } else {
 #pragma unroll
