@@ -454,3 +454,22 @@ def test_read_probe_stays_in_its_rows(qgemv, qtype, M, K):
     torch.cuda.synchronize()
     assert not torch.isnan(y[:M]).any(), "a row was not written"
     assert torch.isnan(y[M:]).all(), "wrote past the rows"
+
+
+def test_launch_floor_runs_eager_and_captured(qgemv):
+    """vx_launch_floor (measurement kernel) launches and completes, eagerly
+    and replayed from a HIP graph, and touches no memory it is not given."""
+    note("launch floor")
+    sentinel = torch.full((1024,), 7.0, device=DEV)
+    for _ in range(3):
+        qgemv.launch_floor()
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(4):
+                qgemv.launch_floor(stream=s)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(sentinel, torch.full((1024,), 7.0, device=DEV))
