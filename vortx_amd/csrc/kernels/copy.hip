@@ -26,6 +26,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_args.hpp"
 
 // q = n / d with a precomputed multiplier (Granlund-Montgomery, as in
 // libdivide's branch-free u32 form): for d >= 2, l = ceil(log2 d),
@@ -38,6 +39,7 @@ __device__ __forceinline__ uint32_t vx_div(uint32_t n, const vx_udiv& d) {
 }
 
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_gen(vx_copy_args a) {
+    vx_args_fetch(a);
     const int64_t off = a.dev_offset ? (int64_t)*a.dev_offset : 0;
     // 64-bit loop index: with total just below 2^32, a u32 i + stride would
     // wrap below total and the loop would never end
@@ -60,6 +62,7 @@ extern "C" __global__ __launch_bounds__(256) void vx_contiguous_gen(vx_copy_args
 // and 16-byte aligned rows (base, offsets and s0..s2 multiples of 4; the host
 // checks): lane i moves elements 4i..4i+3, which share n, c, h.
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_v4(vx_copy_args a) {
+    vx_args_fetch(a);
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     const uint32_t total4 = a.total >> 2;
     const uint64_t stride = (uint64_t)gridDim.x * 256u;
@@ -79,6 +82,7 @@ extern "C" __global__ __launch_bounds__(256) void vx_contiguous_v4(vx_copy_args 
 // grid: x = tiles along w, y = tiles along h, z = n * c slices (loops past
 // the grid limits). Block 256 threads = 4 waves.
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t64(vx_copy_args a) {
+    vx_args_fetch(a);
     __shared__ uint32_t tile[64][65];
     const int64_t off = a.dev_offset ? (int64_t)*a.dev_offset : 0;
     const uint32_t H = a.size[2], W = a.size[3], C = a.size[1];
@@ -161,8 +165,10 @@ __device__ __forceinline__ void vx_contiguous_tile16(const vx_copy_args& a) {
 }
 
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t128(vx_copy_args a) {
+    vx_args_fetch(a);
     vx_contiguous_tile16<128u, 128u>(a);
 }
 extern "C" __global__ __launch_bounds__(256) void vx_contiguous_t128x64(vx_copy_args a) {
+    vx_args_fetch(a);
     vx_contiguous_tile16<128u, 64u>(a);
 }

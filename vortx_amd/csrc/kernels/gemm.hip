@@ -21,6 +21,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_args.hpp"
 #include "vx_dpp.hpp"
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -43,6 +44,7 @@ __device__ __forceinline__ void vx_epilogue(float* c, float acc, float alpha, fl
 
 // ---------------------------------------------------------------- naive
 extern "C" __global__ __launch_bounds__(64) void vx_gemm_naive(vx_gemm_args p) {
+    vx_args_fetch(p);
     const uint32_t j = blockIdx.x * 64u + threadIdx.x;
     const uint32_t i = blockIdx.y;
     const uint32_t z = blockIdx.z;

@@ -1047,9 +1047,13 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     VX_GEMV_BN(QT, QN, 8, 2, 32)                                                                    \
     VX_GEMV_BN(QT, QN, 16, 2, 16)                                                                   \
     extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_generic_##QN(vx_gemv_args a) {     \
+        vx_args_fetch(a);                                                                           \
         vx_gemv_generic<QT>(a);                                                                     \
     }                                                                                               \
-    extern "C" __global__ __launch_bounds__(VX_WG) void vx_dequant_##QN(vx_gemv_args a) { vx_dequant<QT>(a); }
+    extern "C" __global__ __launch_bounds__(VX_WG) void vx_dequant_##QN(vx_gemv_args a) {          \
+        vx_args_fetch(a);                                                                           \
+        vx_dequant<QT>(a);                                                                          \
+    }
 
 VX_GEMV_ALL(VX_Q4_0, q4_0)
 VX_GEMV_ALL(VX_Q8_0, q8_0)
@@ -1068,6 +1072,7 @@ VX_GEMV_P1IE(VX_Q8_0, q8_0)
 VX_GEMV_P1IE(VX_Q4_K, q4_k)
 #define VX_READ_PROBE(QT, QN)                                                                     \
     extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(vx_gemv_args a) {      \
+        vx_args_fetch(a);                                                                         \
         vx_read_probe<QT, 1>(a);                                                                  \
     }
 // Launch floor (measurement only): no work, the batch-1 GEMV's grid. In a

@@ -18,6 +18,7 @@
 #include <stdint.h>
 
 #include "../vx_kargs.h"
+#include "vx_args.hpp"
 #include "vx_dpp.hpp"
 
 #define VX_Q4_0 2
