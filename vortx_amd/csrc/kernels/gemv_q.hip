@@ -171,14 +171,14 @@ __device__ __forceinline__ void vx_gemv_b1(const vx_gemv_args& a) {
 #define VX_P_XF 4096u
 
 template <int QT, int P, int WGT, bool XV, bool XM = false>
-__device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a) {
+__device__ __forceinline__ void vx_gemv_p1(const vx_gemv_args& a, uint32_t G) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr int XPT = (int)(VX_P_XF / WGT);
     const uint32_t t = threadIdx.x, lane = t & 63u;
     // wave-uniform (scalar) so that the item loop runs on scalar branches
     // and the wait counts stay exact
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t G = gridDim.x, nwv = G * (WGT / 64u);
+    const uint32_t nwv = G * (WGT / 64u);
     // waves interleaved over the CUs (wave-major), so the rows left over
     // after whole rounds of nwv spread evenly: at M = 11008 every CU gets 43
     // rows (CU-major numbering gives 176 CUs 48 rows and 80 CUs 32). XM:
@@ -679,14 +679,14 @@ __device__ __forceinline__ void vx_split_store_bn(const vx_i8lds& L, uint32_t f0
 // with more items per wave the x must come first (Q4_0 11008 x 4096 6.38
 // against 6.54 us without the barrier).
 template <int QT, int P, int WGT, bool XV, bool XM = false, bool FS = false, bool EW = false>
-__device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
+__device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a, uint32_t G) {
     constexpr int NW = vx_unit<QT>::NW;
     constexpr uint32_t XW = WGT < 512 ? WGT : 512u;
     constexpr int XPT = (int)(VX_P_XF / XW);
     static_assert(!FS || XPT % 2 == 0, "the paired split takes whole pairs of rounds");
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t G = gridDim.x, nwv = G * (WGT / 64u);
+    const uint32_t nwv = G * (WGT / 64u);
     // XM: workgroups are dealt to the 8 XCDs in turn (workgroup b runs on
     // XCD b % 8), so position pb = (b % 8) G / 8 + b / 8 gives each XCD a
     // contiguous range of positions; with wave-major rows (below) each XCD
@@ -821,11 +821,11 @@ __device__ __forceinline__ void vx_gemv_p1i(const vx_gemv_args& a) {
 // also the fastest depth for the bare loads (Q4_0 11008 x 4096: 6.03 us
 // against 6.13 with two items and 6.34 with four).
 template <int QT, int P>
-__device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a) {
+__device__ __forceinline__ void vx_read_probe(const vx_gemv_args& a, uint32_t G) {
     constexpr int NW = vx_unit<QT>::NW;
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t G = gridDim.x, nwv = G * 16u;
+    const uint32_t nwv = G * 16u;
     const uint32_t pb = (G & 7u) == 0u ? (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
     const uint32_t gw = wave * G + pb;
     const uint32_t nunits = a.nunits, npass = (nunits + 63u) >> 6;
@@ -995,6 +995,36 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
     for (int i = 0; i < 32; ++i) op[(int64_t)i * a.ys_b] = o[i];
 }
 
+// Arguments of the persistent batch-1 kernels (and of the read probe and the
+// launch floor, which mirror them). What a wave needs before its first x and
+// weight requests (W, x, the row stride, M, the units per row, the grid size
+// and the x layout flag) comes first as plain scalars, which the compiler
+// preloads into SGPRs (built with -amdgpu-kernarg-preload-count): the
+// dispatcher writes them with the wave, so no wave waits for a
+// kernel-argument fetch (about 0.3 us, serialized before its first request)
+// before it starts streaming. The rest stays in the vx_gemv_args struct,
+// fetched in the background. The grid size comes in as an argument because
+// gridDim is a hidden argument, not preloaded. Same box, graph-replayed:
+// Q4_0 11008x4096 6.35 -> 5.96 us, Q8_0 4096^2 (_p1e) 5.15 -> 4.88 us,
+// Q4_0 4096x11008 (ring of two) 7.01 -> 6.80 us, Q4_K 14336x4096 7.59 ->
+// 7.28 us, outputs identical. Argument structs themselves cannot be
+// preloaded.
+#define VX_B1_PARAMS                                                                                   \
+    const uint8_t *pre_w, const float *pre_x, uint64_t pre_rs, uint32_t pre_M, uint32_t pre_nu, uint32_t pre_G, \
+        uint32_t pre_xv, vx_gemv_args pre_a
+#define VX_B1_ARGS pre_w, pre_x, pre_rs, pre_M, pre_nu, pre_xv, pre_a
+__device__ __forceinline__ vx_gemv_args vx_b1_args(const uint8_t* w, const float* x, uint64_t rs, uint32_t M,
+                                                   uint32_t nu, uint32_t xv, const vx_gemv_args& a) {
+    vx_gemv_args r = a;
+    r.w = w;
+    r.x = x;
+    r.row_stride = rs;
+    r.M = M;
+    r.nunits = nu;
+    r.x_vec = xv;
+    return r;
+}
+
 #define VX_GEMV_B1(QT, QN, R)                                                              \
     extern "C" __global__ __launch_bounds__(VX_WG) void vx_gemv_b1_##QN##_r##R(vx_gemv_args a) { \
         if (a.x_vec) vx_gemv_b1<QT, R, true>(a);                                           \
@@ -1019,19 +1049,23 @@ __device__ __forceinline__ void vx_dequant(const vx_gemv_args& a) {
 // 7.72 / 6.61 / 8.71 / 9.92 / 18.49, ring 1 with XM 6.57 / 5.47 / 7.96 /
 // 8.34 / 15.85. Outputs identical bit for bit across all of them.
 #define VX_GEMV_P1(QT, QN, P, WGT)                                                              \
-    extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(vx_gemv_args a) {  \
-        if (a.x_vec) vx_gemv_p1<QT, P, WGT, true, true>(a); else vx_gemv_p1<QT, P, WGT, false, true>(a); \
+    extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(VX_B1_PARAMS) {     \
+        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                              \
+        if (pre_xv) vx_gemv_p1<QT, P, WGT, true, true>(a, pre_G);                                   \
+        else vx_gemv_p1<QT, P, WGT, false, true>(a, pre_G);                                         \
     }
 #define VX_GEMV_P1I(QT, QN, P)                                                                  \
-    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(vx_gemv_args a) {  \
-        if (a.x_vec) vx_gemv_p1i<QT, P, 1024, true, true, true>(a);                              \
-        else vx_gemv_p1i<QT, P, 1024, false, true, true>(a);                                     \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(VX_B1_PARAMS) {     \
+        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                            \
+        if (pre_xv) vx_gemv_p1i<QT, P, 1024, true, true, true>(a, pre_G);                         \
+        else vx_gemv_p1i<QT, P, 1024, false, true, true>(a, pre_G);                               \
     }
 // _p1e: one item per wave (every row one pass, at most one row per wave)
 #define VX_GEMV_P1IE(QT, QN)                                                                    \
-    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p1e(vx_gemv_args a) {   \
-        if (a.x_vec) vx_gemv_p1i<QT, 1, 1024, true, true, true, true>(a);                        \
-        else vx_gemv_p1i<QT, 1, 1024, false, true, true, true>(a);                               \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p1e(VX_B1_PARAMS) {      \
+        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                            \
+        if (pre_xv) vx_gemv_p1i<QT, 1, 1024, true, true, true, true>(a, pre_G);                   \
+        else vx_gemv_p1i<QT, 1, 1024, false, true, true, true>(a, pre_G);                         \
     }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \
@@ -1071,15 +1105,15 @@ VX_GEMV_P1IE(VX_Q4_0, q4_0)
 VX_GEMV_P1IE(VX_Q8_0, q8_0)
 VX_GEMV_P1IE(VX_Q4_K, q4_k)
 #define VX_READ_PROBE(QT, QN)                                                                     \
-    extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(vx_gemv_args a) {      \
-        vx_args_fetch(a);                                                                         \
-        vx_read_probe<QT, 1>(a);                                                                  \
+    extern "C" __global__ __launch_bounds__(1024) void vx_read_probe_##QN(VX_B1_PARAMS) {         \
+        vx_read_probe<QT, 1>(vx_b1_args(VX_B1_ARGS), pre_G);                                      \
     }
-// Launch floor (measurement only): no work, the batch-1 GEMV's grid. In a
-// replayed HIP graph its time per launch is the fixed cost every kernel of
-// a step pays (dispatch, wave launch, completion) before any byte moves.
-extern "C" __global__ __launch_bounds__(1024) void vx_launch_floor_k(vx_gemv_args a) {
-    if (a.M == 0xFFFFFFFFu && threadIdx.x == 0) a.y[blockIdx.x] = 0.f;  // never true: keeps the argument
+// Launch floor (measurement only): no work, the batch-1 GEMV's grid and
+// preloaded arguments. In a replayed HIP graph its time per launch is the
+// fixed cost every kernel of a step pays (dispatch with its argument
+// preload, wave launch, completion) before any byte moves.
+extern "C" __global__ __launch_bounds__(1024) void vx_launch_floor_k(VX_B1_PARAMS) {
+    if (pre_M == 0xFFFFFFFFu && threadIdx.x == 0) pre_a.y[blockIdx.x] = 0.f;  // never true: keeps the argument
 }
 VX_READ_PROBE(VX_Q4_0, q4_0)
 VX_READ_PROBE(VX_Q8_0, q8_0)

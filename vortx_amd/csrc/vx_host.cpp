@@ -103,11 +103,10 @@ struct DeviceGuard {
     }
 };
 
-// Every kernel takes one argument: its vx_*_args struct by value. It is
-// passed through kernelParams (an array of pointers to each argument), which
-// the runtime copies by the kernel's argument layout at launch, and which
-// stream capture copies into the graph node, so the struct may live on this
-// stack frame.
+// Every kernel takes its vx_*_args struct by value. It is passed through
+// kernelParams (an array of pointers to each argument), which the runtime
+// copies by the kernel's argument layout at launch, and which stream capture
+// copies into the graph node, so the arguments may live on this stack frame.
 template <class Args>
 static int launch(vx_ctx ctx, int k, dim3 grid, dim3 block, size_t lds, vx_stream stream, const Args& args) {
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return VX_OK;
@@ -115,6 +114,24 @@ static int launch(vx_ctx ctx, int k, dim3 grid, dim3 block, size_t lds, vx_strea
     void* params[] = {&copy};
     const hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                                (unsigned)lds, (hipStream_t)stream, params, nullptr);
+    if (e != hipSuccess) return fail_hip(e, kKernelNames[k]);
+    return VX_OK;
+}
+
+// The persistent batch-1 kernels (and the read probe and launch floor) take
+// the fields a wave needs before its first request as leading scalars, which
+// arrive preloaded in SGPRs (VX_B1_PARAMS in gemv_q.hip: w, x, row stride,
+// M, units per row, grid size, x layout flag), then the struct.
+static int launch_b1(vx_ctx ctx, int k, uint32_t grid, size_t lds, vx_stream stream, const vx_gemv_args& args) {
+    if (grid == 0) return VX_OK;
+    vx_gemv_args copy = args;
+    const uint8_t* w = args.w;
+    const float* x = args.x;
+    uint64_t rs = args.row_stride;
+    uint32_t M = args.M, nu = args.nunits, G = grid, xv = args.x_vec;
+    void* params[] = {&w, &x, &rs, &M, &nu, &G, &xv, &copy};
+    const hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid, 1, 1, 1024, 1, 1, (unsigned)lds, (hipStream_t)stream,
+                                               params, nullptr);
     if (e != hipSuccess) return fail_hip(e, kKernelNames[k]);
     return VX_OK;
 }
@@ -905,7 +922,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             // One item per wave: no barrier between the x and the weight
             // requests (_p1e; Q8_0 4096 x 4096 5.37 -> 5.15 us).
             const int ring = items == 1u ? 0 : (npass == 1u || (w->qtype == VX_Q8_0 && items <= 2u)) ? 1 : 2;
-            s = launch(ctx, p1i_kernel(w->qtype, ring), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
+            s = launch_b1(ctx, p1i_kernel(w->qtype, ring), (uint32_t)ctx->num_cus, lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
@@ -926,7 +943,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
             lds = (size_t)16u * a.upitch * 16u + (size_t)a.nunits * 8u;
-            s = launch(ctx, p1_kernel(w->qtype), dim3((uint32_t)ctx->num_cus), dim3(1024u), lds, stream, a);
+            s = launch_b1(ctx, p1_kernel(w->qtype), (uint32_t)ctx->num_cus, lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
@@ -986,7 +1003,7 @@ static int run_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w, flo
     a.nunits = w->cols / 64u;
     const int k = q_index(w->qtype) == 0 ? K_vx_read_probe_q4_0 : q_index(w->qtype) == 1 ? K_vx_read_probe_q8_0
                                                                                          : K_vx_read_probe_q4_k;
-    return launch(ctx, k, dim3((uint32_t)ctx->num_cus), dim3(1024u), 0, stream, a);
+    return launch_b1(ctx, k, (uint32_t)ctx->num_cus, 0, stream, a);
 }
 
 // Launch floor: an empty kernel on the batch-1 GEMV's grid (measurement).
@@ -995,7 +1012,7 @@ static int run_launch_floor(vx_ctx ctx, vx_stream stream) {
     if (!ctx) return fail(VX_ERR_INVALID, "null ctx");
     DeviceGuard guard(ctx->device);
     vx_gemv_args a{};
-    return launch(ctx, K_vx_launch_floor_k, dim3((uint32_t)ctx->num_cus), dim3(1024u), 0, stream, a);
+    return launch_b1(ctx, K_vx_launch_floor_k, (uint32_t)ctx->num_cus, 0, stream, a);
 }
 
 // ------------------------------------------------------------ contiguous
