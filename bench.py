@@ -19,15 +19,21 @@ GEMM shapes and the broadcast batch; then the GGUF upload, the reference's
 GEMM size sweep (examples/gemm_bench.rs: 64..4096, tiled and naive) and
 CPU baselines from the oracle's OpenMP restatements on the host cores.
 
-Timing: exactly K steps replayed from HIP graphs of captured launches
-between two synchronizations; the timed region is bracketed by HIP events
-recorded on the stream the kernels run on, and `ms_per_step` / `value` /
-`roofline.achieved` are that region's duration per step and the algorithmic
-bytes (or flops) over it (a two-launch batched step counts both launches;
-its GEMV kernel alone is reported as `gemv_only`). `wall_ms_per_step` is
-the wall clock between the two synchronizations per step (host-side graph
-launch and synchronization included). A graph replay carries ~8-10 us of its
-own, so short runs (--steps 20) read ~0.4 us per step above long ones.
+Timing: exactly K steps between two synchronizations; the timed region is
+bracketed by HIP events recorded on the stream the kernels run on, and
+`ms_per_step` / `value` / `roofline.achieved` are that region's duration per
+step and the algorithmic bytes (or flops) over it (a two-launch batched step
+counts both launches; its GEMV kernel alone is reported as `gemv_only`). Up
+to 256 steps the launches are issued directly on the stream behind a short
+spin kernel queued ahead of the start event (the "blocking kernel" of
+NVBench), so the host has queued every launch before the GPU reaches the
+start event and the region holds GPU time only; each run checks that this
+held (the start event still pending once all launches are queued) and
+otherwise retries with a longer spin. Longer runs replay HIP graphs of up to
+500 captured launches (a graph replay carries ~9.5 us of its own on the GPU,
+measured: at 20 launches per replay 0.47 us per step, at 500 0.02).
+`wall_ms_per_step` is the wall clock between the two synchronizations per
+step (host-side launches and synchronization included, the spin excluded).
 rocprofv3 summaries of the same command are kept under profiles/. Nothing
 goes to stderr without --verbose.
 
@@ -96,19 +102,51 @@ def per_step(done: int, wall: float, ev_ms: float, work: float, scale: float = 1
             "wall_ms_per_step": wall * 1e3 / done}
 
 
+EAGER_MAX = 256  # at most this many timed steps: direct launches behind a spin kernel
+
+
 def graph_time(launch, steps: int):
-    """Exactly `steps` launches (launch(i, stream)) on a side stream, captured
-    min(steps, 500) at a time into a HIP graph (the remainder into a second
-    one) and replayed between two synchronizations after one untimed replay;
-    HIP events on that stream bracket exactly the timed launches. Each replay
-    carries ~8-10 us of its own on the GPU (at 20 steps of a 6.4 us kernel,
-    0.4-0.5 us per step; at 500, 0.02). Returns (launches done, wall seconds
-    between the synchronizations, HIP-event ms of the timed launches)."""
+    """Exactly `steps` launches (launch(i, stream)) on a side stream, timed by
+    HIP events on that stream between two synchronizations (one untimed pass
+    first). Up to EAGER_MAX steps: a spin kernel (torch.cuda._sleep), the
+    start event, the launches, the end event, so that the host has queued
+    every launch before the GPU reaches the start event; the start event still
+    pending after the last launch is queued shows it (else the spin is made
+    four times longer and the run repeated). Longer runs: HIP graphs of
+    min(steps, 500) captured launches (the remainder in a second graph),
+    replayed. Returns (launches done, wall seconds between the
+    synchronizations less the spin, HIP-event ms of the timed launches)."""
     import torch
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if steps <= EAGER_MAX:
+        es = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            for i in range(steps):  # untimed pass (also the host's cost per launch)
+                launch(i, s)
+        torch.cuda.synchronize()
+        cycles = 4_000_000
+        for _ in range(4):
+            with torch.cuda.stream(s):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                es.record(s)
+                torch.cuda._sleep(cycles)
+                e0.record(s)
+                for i in range(steps):
+                    launch(i, s)
+                covered = not e0.query()
+                e1.record(s)
+                torch.cuda.synchronize()
+            wall = time.perf_counter() - t0 - es.elapsed_time(e0) * 1e-3
+            if covered:
+                break
+            cycles *= 4
+        else:
+            raise RuntimeError("the spin kernel never outlasted the host's launches")
+        return steps, max(wall, 0.0), e0.elapsed_time(e1)
     chunk = min(steps, 500)
     reps, rem = divmod(steps, chunk)
     graphs = []
@@ -695,7 +733,8 @@ def main() -> int:
         "config": {"workload": "Q4_0 GEMV y=Wx, W 11008x4096 (GGML Q4_0 blocks), batch 1",
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
                    "bytes_per_step": q40["alg_bytes"],
-                   "timing": "HIP-graph replay of eager launches, HIP events around exactly the timed steps",
+                   "timing": ("HIP events around exactly the timed steps; <= %d steps: direct launches queued behind a "
+                              "spin kernel, else HIP-graph replay" % EAGER_MAX),
                    "x_repr": X_REPR},
         "roofline": roof(q40, "gemv_q4_0_11008x4096_b1"),
         "cpu_baseline": cpu["q4_0"] if cpu else None,
