@@ -24,12 +24,13 @@ bracketed by HIP events recorded on the stream the kernels run on, and
 `ms_per_step` / `value` / `roofline.achieved` are that region's duration per
 step and the algorithmic bytes (or flops) over it (a two-launch batched step
 counts both launches; its GEMV kernel alone is reported as `gemv_only`). Up
-to 256 steps the launches are issued directly on the stream behind a short
-spin kernel queued ahead of the start event (the "blocking kernel" of
-NVBench), so the host has queued every launch before the GPU reaches the
-start event and the region holds GPU time only; each run checks that this
-held (the start event still pending once all launches are queued) and
-otherwise retries with a longer spin. Longer runs replay HIP graphs of up to
+to 256 steps (the headline at the driver's --steps 20) the launches are
+issued directly on the stream behind a short spin kernel queued ahead of the
+start event (the "blocking kernel" of NVBench), so the host has queued every
+launch before the GPU reaches the start event and the region holds GPU time
+only; each run checks that this held (the start event still pending once all
+launches are queued) and otherwise retries with a longer spin. Longer runs,
+and every other line (at least 1000 launches), replay HIP graphs of up to
 500 captured launches (a graph replay carries ~9.5 us of its own on the GPU,
 measured: at 20 launches per replay 0.47 us per step, at 500 0.02).
 `wall_ms_per_step` is the wall clock between the two synchronizations per
@@ -124,7 +125,7 @@ def graph_time(launch, steps: int):
     if steps <= EAGER_MAX:
         es = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(s):
-            for i in range(steps):  # untimed pass (also the host's cost per launch)
+            for i in range(steps):  # untimed pass
                 launch(i, s)
         torch.cuda.synchronize()
         cycles = 4_000_000
@@ -583,7 +584,7 @@ GEMM_STEPS, GEMM_WARMUP = 50, 50
 def run_workloads(keys, steps: int, warmup: int) -> dict:
     """Run the named workloads in KEYS order; returns key -> result. The
     headline takes exactly `steps` timed steps after `warmup`; the other lines
-    take at least 1000 launches (GEMV-sized) or 50 (GEMMs)."""
+    take at least 1000 launches (GEMV-sized, graph-replayed) or 50 (GEMMs)."""
     out = {}
     many = max(1000, steps)
     for k in [k for k in KEYS if k in keys]:
