@@ -332,8 +332,9 @@ int vx_gemv_q_noalloc(vx_ctx ctx, vx_stream stream, const vx_mview* y,
 
 /* Measurement only, no counterpart in the reference: the loads of the
  * batch-1 GEMV (vx_gemv_q at B = 1) with nothing else — the same grid, row
- * order and per-lane 64-weight units, one item per wave in flight (the
- * GEMV's ring for K <= 4096), no x, no barrier, no arithmetic. Reads every byte of W once and
+ * order, per-lane 64-weight units and preloaded kernel arguments, one item
+ * per wave in flight (the GEMV's ring for K <= 4096), no x, no barrier, no
+ * arithmetic. Reads every byte of W once and
  * writes one word per row to y[0..M) (contents unspecified). Its time is
  * the ceiling of what that access pattern streams in one launch. Needs K a
  * multiple of 64 and 4-byte aligned rows (else VX_ERR_UNSUPPORTED). */
@@ -342,8 +343,9 @@ int vx_gemv_q_read_probe(vx_ctx ctx, vx_stream stream, const vx_qweight* w,
 
 /* Measurement only, no counterpart in the reference: one launch of an
  * empty kernel on the batch-1 GEMV's grid (one workgroup of 1024 threads
- * per CU). Its time per launch in a replayed HIP graph is the fixed cost of
- * any launch on this device, the floor under every per-step time. */
+ * per CU) with its preloaded kernel arguments. Its time per launch in a
+ * replayed HIP graph is the fixed cost of such a launch on this device, the
+ * floor under every per-step time of the batch-1 GEMV. */
 int vx_launch_floor(vx_ctx ctx, vx_stream stream);
 
 /* out[m, k] = W[m, k] decoded to f32 (bit-exact: every block value is
