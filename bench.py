@@ -122,7 +122,7 @@ def graph_time(launch, steps: int):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    if steps <= EAGER_MAX:
+    if steps <= EAGER_MAX and hasattr(torch.cuda, "_sleep"):  # (a private torch helper: else graphs)
         es = torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(s):
             for i in range(steps):  # untimed pass
