@@ -1048,24 +1048,31 @@ __device__ __forceinline__ vx_gemv_args vx_b1_args(const uint8_t* w, const float
 // 14.69, ring 2 with both 6.90 / 5.50 / 7.82 / 8.27 / 14.99; f32 x, ring 2
 // 7.72 / 6.61 / 8.71 / 9.92 / 18.49, ring 1 with XM 6.57 / 5.47 / 7.96 /
 // 8.34 / 15.85. Outputs identical bit for bit across all of them.
+// One kernel per x layout (contiguous x: the default; _xs: strided x): with
+// both bodies in one kernel behind a run-time flag the contiguous path ran
+// slower (same box, graph-replayed: Q4_0 11008x4096 6.18 against 6.06 us,
+// 4096x11008 ring of two 7.03 against 6.72 us).
 #define VX_GEMV_P1(QT, QN, P, WGT)                                                              \
     extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT(VX_B1_PARAMS) {     \
-        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                              \
-        if (pre_xv) vx_gemv_p1<QT, P, WGT, true, true>(a, pre_G);                                   \
-        else vx_gemv_p1<QT, P, WGT, false, true>(a, pre_G);                                         \
+        vx_gemv_p1<QT, P, WGT, true, true>(vx_b1_args(VX_B1_ARGS), pre_G);                          \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(WGT) void vx_gemv_p1_##QN##_w##WGT##_xs(VX_B1_PARAMS) { \
+        vx_gemv_p1<QT, P, WGT, false, true>(vx_b1_args(VX_B1_ARGS), pre_G);                         \
     }
 #define VX_GEMV_P1I(QT, QN, P)                                                                  \
     extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P(VX_B1_PARAMS) {     \
-        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                            \
-        if (pre_xv) vx_gemv_p1i<QT, P, 1024, true, true, true>(a, pre_G);                         \
-        else vx_gemv_p1i<QT, P, 1024, false, true, true>(a, pre_G);                               \
+        vx_gemv_p1i<QT, P, 1024, true, true, true>(vx_b1_args(VX_B1_ARGS), pre_G);                \
+    }                                                                                             \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p##P##_xs(VX_B1_PARAMS) { \
+        vx_gemv_p1i<QT, P, 1024, false, true, true>(vx_b1_args(VX_B1_ARGS), pre_G);              \
     }
 // _p1e: one item per wave (every row one pass, at most one row per wave)
 #define VX_GEMV_P1IE(QT, QN)                                                                    \
     extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p1e(VX_B1_PARAMS) {      \
-        const vx_gemv_args a = vx_b1_args(VX_B1_ARGS);                                            \
-        if (pre_xv) vx_gemv_p1i<QT, 1, 1024, true, true, true, true>(a, pre_G);                   \
-        else vx_gemv_p1i<QT, 1, 1024, false, true, true, true>(a, pre_G);                         \
+        vx_gemv_p1i<QT, 1, 1024, true, true, true, true>(vx_b1_args(VX_B1_ARGS), pre_G);          \
+    }                                                                                             \
+    extern "C" __global__ __launch_bounds__(1024) void vx_gemv_p1i_##QN##_p1e_xs(VX_B1_PARAMS) {   \
+        vx_gemv_p1i<QT, 1, 1024, false, true, true, true>(vx_b1_args(VX_B1_ARGS), pre_G);        \
     }
 #define VX_GEMV_ALL(QT, QN)                                                                         \
     VX_GEMV_B1(QT, QN, 1)                                                                           \

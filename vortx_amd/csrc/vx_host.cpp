@@ -500,23 +500,25 @@ static int bn_kernel(uint32_t qt, int NB) {
     return tab[q_index(qt)][ni];
 }
 
-// Persistent batch-1 kernel with f32 x (VX_GEMV_X_F32).
-static int p1_kernel(uint32_t qt) {
-    static const int tab[3] = {K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q4_k_w1024};
-    return tab[q_index(qt)];
+// Persistent batch-1 kernel with f32 x (VX_GEMV_X_F32); xv: x contiguous
+// along K and 16-byte aligned (else the _xs form, strided x).
+static int p1_kernel(uint32_t qt, bool xv) {
+    static const int tab[2][3] = {{K_vx_gemv_p1_q4_0_w1024_xs, K_vx_gemv_p1_q8_0_w1024_xs, K_vx_gemv_p1_q4_k_w1024_xs},
+                                  {K_vx_gemv_p1_q4_0_w1024, K_vx_gemv_p1_q8_0_w1024, K_vx_gemv_p1_q4_k_w1024}};
+    return tab[xv ? 1 : 0][q_index(qt)];
 }
 
 // Persistent batch-1 kernel on the integer-dot path, by ring depth P (1 or
-// 2); P = 0: the one-item-per-wave form (_p1e).
-static int p1i_kernel(uint32_t qt, int P) {
-    if (P == 0)
-        return q_index(qt) == 0 ? K_vx_gemv_p1i_q4_0_p1e : q_index(qt) == 1 ? K_vx_gemv_p1i_q8_0_p1e
-                                                                             : K_vx_gemv_p1i_q4_k_p1e;
-    switch (q_index(qt)) {
-    case 0: return P >= 2 ? K_vx_gemv_p1i_q4_0_p2 : K_vx_gemv_p1i_q4_0_p1;
-    case 1: return P >= 2 ? K_vx_gemv_p1i_q8_0_p2 : K_vx_gemv_p1i_q8_0_p1;
-    default: return P >= 2 ? K_vx_gemv_p1i_q4_k_p2 : K_vx_gemv_p1i_q4_k_p1;
-    }
+// 2; P = 0: the one-item-per-wave form, _p1e) and x layout (as p1_kernel).
+static int p1i_kernel(uint32_t qt, int P, bool xv) {
+    static const int tab[2][3][3] = {
+        {{K_vx_gemv_p1i_q4_0_p1e_xs, K_vx_gemv_p1i_q4_0_p1_xs, K_vx_gemv_p1i_q4_0_p2_xs},
+         {K_vx_gemv_p1i_q8_0_p1e_xs, K_vx_gemv_p1i_q8_0_p1_xs, K_vx_gemv_p1i_q8_0_p2_xs},
+         {K_vx_gemv_p1i_q4_k_p1e_xs, K_vx_gemv_p1i_q4_k_p1_xs, K_vx_gemv_p1i_q4_k_p2_xs}},
+        {{K_vx_gemv_p1i_q4_0_p1e, K_vx_gemv_p1i_q4_0_p1, K_vx_gemv_p1i_q4_0_p2},
+         {K_vx_gemv_p1i_q8_0_p1e, K_vx_gemv_p1i_q8_0_p1, K_vx_gemv_p1i_q8_0_p2},
+         {K_vx_gemv_p1i_q4_k_p1e, K_vx_gemv_p1i_q4_k_p1, K_vx_gemv_p1i_q4_k_p2}}};
+    return tab[xv ? 1 : 0][q_index(qt)][P <= 0 ? 0 : P >= 2 ? 2 : 1];
 }
 
 static int generic_kernel(uint32_t qt) {
@@ -922,7 +924,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             // One item per wave: no barrier between the x and the weight
             // requests (_p1e; Q8_0 4096 x 4096 5.37 -> 5.15 us).
             const int ring = items == 1u ? 0 : (npass == 1u || (w->qtype == VX_Q8_0 && items <= 2u)) ? 1 : 2;
-            s = launch_b1(ctx, p1i_kernel(w->qtype, ring), (uint32_t)ctx->num_cus, lds, stream, a);
+            s = launch_b1(ctx, p1i_kernel(w->qtype, ring, a.x_vec != 0), (uint32_t)ctx->num_cus, lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
@@ -943,7 +945,7 @@ static int run_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y, const vx_
             a.chunk_units = a.nunits;
             a.upitch = a.nunits | 1u;
             lds = (size_t)16u * a.upitch * 16u + (size_t)a.nunits * 8u;
-            s = launch_b1(ctx, p1_kernel(w->qtype), (uint32_t)ctx->num_cus, lds, stream, a);
+            s = launch_b1(ctx, p1_kernel(w->qtype, a.x_vec != 0), (uint32_t)ctx->num_cus, lds, stream, a);
             if (s) return s;
             b0 += NB;
             continue;
