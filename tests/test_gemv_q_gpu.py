@@ -281,6 +281,31 @@ def test_gemv_generic_paths(qgemv, qtype):
 
 
 @pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+@pytest.mark.parametrize("x_f32", [False, True], ids=["int8x", "f32x"])
+# on 256 CUs: one item per wave (_p1e), two one-pass items (ring of one),
+# two and three passes (ring of two; Q8_0 with two items: ring of one)
+@pytest.mark.parametrize("M,K", [(300, 4096), (5000, 4096), (600, 8192), (131, 11008)])
+def test_gemv_b1_strided_x_matches_contiguous(qgemv, qtype, x_f32, M, K):
+    """Batch 1 with x not contiguous along K (stride 3) runs the strided-x
+    (_xs) form of the persistent kernels: y equals the contiguous-x run bit
+    for bit (the same values staged and split in the same order) and the
+    oracle within tolerance."""
+    note(f"gemv b=1 strided-x {QN[qtype]} {M}x{K} x_f32={x_f32}")
+    w = S.quant_weights(qtype, M, K, seed=31, device=DEV)
+    x = S.activations(1, K, seed=32, device=DEV)
+    qw = vx.QWeight(w, qtype, M, K)
+    y0 = torch.full((1, M), float("nan"), device=DEV)
+    qgemv.dispatch(y0.t(), qw, x.t(), x_f32=x_f32)
+    xk3 = torch.full((K, 3), float("nan"), device=DEV)
+    xk3[:, 0] = x[0]
+    y1 = torch.full((1, M), float("nan"), device=DEV)
+    qgemv.dispatch(y1.t(), qw, xk3[:, :1], x_f32=x_f32)
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int32), y1.view(torch.int32))
+    assert_close(y1.t().cpu().numpy(), O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy()))
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
 def test_gemv_strided_x_fast_weights(qgemv, qtype):
     """Aligned weights with x not contiguous along K (scalar staging)."""
     M, K, B = 64, 4096, 2
