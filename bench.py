@@ -151,7 +151,8 @@ class HipEvent:
         return ms.value
 
     def __del__(self):
-        if HipEvent._hip is not None and self.h:
+        # not during interpreter shutdown, when the HIP runtime may be gone
+        if HipEvent._hip is not None and self.h and not sys.is_finalizing():
             HipEvent._hip.hipEventDestroy(self.h)
 
 
