@@ -498,3 +498,39 @@ def test_launch_floor_runs_eager_and_captured(qgemv):
         g.replay()
     torch.cuda.synchronize()
     assert torch.equal(sentinel, torch.full((1024,), 7.0, device=DEV))
+
+
+@pytest.mark.parametrize("qtype", QTYPES, ids=lambda q: QN[q])
+def test_gemv_empty_shapes(qgemv, qtype):
+    """Empty shapes, as the GEMM treats them (K = 0 writes zeros, nothing to
+    write is a no-op): K = 0 gives y = 0 at B = 1 and B = 3 (with and without
+    a workspace, int8 and f32 x); M = 0 and B = 0 launch nothing and return
+    success; dequantize of 0 rows likewise. A normal call afterwards still
+    matches the oracle."""
+    qk, bb = O.QTYPE_INFO[qtype]
+    M, K = 70, 2 * qk if qtype == vx.VX_Q4_K else 256
+    note(f"gemv empty shapes {QN[qtype]}")
+    w0 = vx.QWeight(torch.empty((M, 0), dtype=torch.uint8, device=DEV), qtype, M, 0)
+    for B in (1, 3):
+        for x_f32 in (False, True):
+            x = torch.empty((B, 0), device=DEV)
+            for ws in (None, vx.QuantGemv.workspace(w0, B)):
+                y = torch.full((B, M), float("nan"), device=DEV)
+                qgemv.dispatch(y[0] if B == 1 else y.t(), w0, x[0] if B == 1 else x.t(), x_f32=x_f32, workspace=ws)
+                torch.cuda.synchronize()
+                assert (y == 0).all(), f"K = 0 must write zeros (B={B}, x_f32={x_f32}, workspace={ws is not None})"
+    wm = vx.QWeight(torch.empty((0, K // qk * bb), dtype=torch.uint8, device=DEV), qtype, 0, K)
+    qgemv.dispatch(torch.empty(0, device=DEV), wm, S.activations(1, K, seed=3, device=DEV)[0])
+    qgemv.dispatch(torch.empty((3, 0), device=DEV).t(), wm, S.activations(3, K, seed=4, device=DEV).t())
+    qgemv.dequantize(torch.empty((0, K), device=DEV), wm)
+    w = S.quant_weights(qtype, M, K, seed=5, device=DEV)
+    qw = vx.QWeight(w, qtype, M, K)
+    y = torch.full((M, 0), float("nan"), device=DEV)
+    qgemv.dispatch(y, qw, torch.empty((K, 0), device=DEV))
+    qgemv.dispatch(y, qw, torch.empty((K, 0), device=DEV), workspace=vx.QuantGemv.workspace(qw, 4))
+    # the library is still in a good state
+    x = S.activations(2, K, seed=6, device=DEV)
+    y = torch.full((2, M), float("nan"), device=DEV)
+    qgemv.dispatch(y.t(), qw, x.t())
+    torch.cuda.synchronize()
+    assert_close(y.cpu().numpy().T, O.gemv_q_f64(qtype, w.cpu().numpy(), M, K, x.cpu().numpy()))
