@@ -217,6 +217,11 @@ int vx_gemm_f32_route(const vx_mview* out, const vx_cview* lhs,
  * point has none, so they are computed with x kept in f32 (the
  * VX_GEMV_X_F32 kernels); vx_gemv_q_ws with a caller workspace keeps the
  * int8 split there (the fused and the two-launch route give the same bits).
+ * Empty shapes: K = 0 writes y = 0 (as vx_gemm_f32 with K = 0); M = 0 or
+ * B = 0 returns VX_OK and launches nothing. The same holds for _ex, _ws
+ * and _noalloc; vx_gemv_q_xq also returns VX_OK for M = 0 or B = 0 but
+ * refuses K = 0 (VX_ERR_UNSUPPORTED), and vx_dequantize of 0 rows is a
+ * no-op.
  * Uses no memory beyond its operands; safe to call concurrently on any
  * streams, and to capture. */
 int vx_gemv_q(vx_ctx ctx, vx_stream stream, const vx_mview* y,
