@@ -189,6 +189,23 @@ def test_special_cases(gemm):
     assert np.array_equal(c.cpu().numpy(), exact)
 
 
+def test_empty_outputs_are_no_ops(gemm):
+    """M = 0, N = 0 or an empty batch: nothing to write, success, no launch
+    (the route is VX_ROUTE_EMPTY); a normal call afterwards is exact."""
+    note("gemm empty outputs")
+    for M, N, K in ((0, 50, 40), (40, 0, 40), (0, 0, 0)):
+        gemm.dispatch(torch.empty((M, N), device=DEV), torch.empty((M, K), device=DEV), torch.empty((K, N), device=DEV))
+    gemm.dispatch(torch.empty((0, 3, 4), device=DEV), torch.empty((0, 3, 5), device=DEV),
+                  torch.empty((0, 5, 4), device=DEV))
+    ai = torch.randint(-8, 9, (40, 24), generator=torch.Generator().manual_seed(5)).float().to(DEV)
+    bi = torch.randint(-8, 9, (24, 36), generator=torch.Generator().manual_seed(6)).float().to(DEV)
+    c = _nan(40, 36)
+    gemm.dispatch(c, ai, bi)
+    torch.cuda.synchronize()
+    exact = (ai.cpu().numpy().astype(np.int64) @ bi.cpu().numpy().astype(np.int64)).astype(np.float32)
+    assert np.array_equal(c.cpu().numpy(), exact)
+
+
 def test_shape_mismatch_is_an_error(gemm):
     a = torch.zeros((40, 30), device=DEV)
     b = torch.zeros((31, 50), device=DEV)
