@@ -784,7 +784,7 @@ def main() -> int:
         "config": {"workload": "Q4_0 GEMV y=Wx, W 11008x4096 (GGML Q4_0 blocks), batch 1",
                    "M": 11008, "K": 4096, "batch": 1, "weight_copies": q40["weight_copies"],
                    "bytes_per_step": q40["alg_bytes"],
-                   "timing": ("HIP events around exactly the timed steps; <= %d steps: direct launches queued behind a "
+                   "timing": ("timing-only HIP events (hipEventDisableSystemFence) around exactly the timed steps; <= %d steps: direct launches queued behind a "
                               "spin kernel, else HIP-graph replay" % EAGER_MAX),
                    "x_repr": X_REPR},
         "roofline": roof(q40, "gemv_q4_0_11008x4096_b1"),
