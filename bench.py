@@ -9,8 +9,8 @@ cannot serve them), inputs resident in HBM before timing starts.
 Beside it, top-level objects for the metric's other halves and the
 ceiling: Q8_0 4096 x 4096 b=1, the headline with x kept in f32, the read
 probe (the headline GEMV's loads of W alone: the most its access pattern
-can stream in one launch) and the f32 GEMM 4096^3 (TFLOP/s, >= 50 timed
-launches after 10 warmups). Compact lines ([value, ms per step, roofline
+can stream in one launch) and the f32 GEMM 4096^3 (TFLOP/s, 50 timed
+launches after 50 warmups). Compact lines ([value, ms per step, roofline
 achieved, roofline frac, launches per step]) cover the other BASELINE GEMV
 configs, the activation split kernel alone, the f32 GEMV as a read-only
 stream (headline size, 537 MB), copies (transposed 8192^2 view, contiguous
